@@ -1,0 +1,21 @@
+"""clove_compute_amd -- MI355X (gfx950) GEMM hot path of Clove Compute.
+
+The product is the C ABI library ``lib/libclove_gemm.so`` (declared in
+include/clove/gemm_c.h, C++ spelling in include/clove/gemm.h).  This package
+is its Python host side: the ctypes binding, a mirror of the reference's
+GEMM API over torch device tensors, and the INT4 packing/quantisation helpers.
+"""
+from ._lib import CloveError, CLOVE_INT4_GROUPWISE, CLOVE_INT4_REFERENCE_LITERAL  # noqa: F401
+from .gemm import (  # noqa: F401
+    INT4_GROUP_SIZE,
+    gemm_fp16,
+    gemm_fp16_batched,
+    gemm_int4,
+    gemm_int4_ex,
+    gemm_int8,
+    gemm_int8_acc32,
+    gemm_int8_rowcol,
+    gemm_w4a16,
+    release_scratch,
+)
+from . import quant  # noqa: F401

@@ -1,0 +1,292 @@
+// C ABI of the gfx950 GEMM library: argument validation, per-stream scratch,
+// dispatch to the kernel launchers.  Declarations and the reference interface
+// each entry point replaces: include/clove/gemm_c.h.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+#include <vector>
+
+#include "clove/gemm_c.h"
+#include "common.hpp"
+#include "dispatch.hpp"
+
+namespace clove {
+using hw::cdiv64;
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+// ---------------------------------------------------------------------------
+// device info (cached per device)
+// ---------------------------------------------------------------------------
+std::mutex g_dev_mu;
+std::map<int, int> g_num_cus;
+
+// ---------------------------------------------------------------------------
+// scratch per (device, stream)
+// ---------------------------------------------------------------------------
+struct ScratchEntry {
+    void* base = nullptr;
+    Scratch view;
+};
+std::mutex g_scratch_mu;
+std::map<std::pair<int, void*>, ScratchEntry> g_scratch;
+
+__global__ void zero_u32(unsigned* p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+size_t round_up_pow2(size_t x, size_t floor_bytes) {
+    size_t r = floor_bytes;
+    while (r < x) r <<= 1;
+    return r;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    if (!a || !b || abytes == 0 || bbytes == 0) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+
+}  // namespace
+
+clove_status_t current_device_info(DeviceInfo* out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    auto it = g_num_cus.find(dev);
+    if (it == g_num_cus.end()) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            return CLOVE_ERR_NO_DEVICE;
+        it = g_num_cus.emplace(dev, cus).first;
+    }
+    out->device = dev;
+    out->num_cus = it->second;
+    return CLOVE_OK;
+}
+
+clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t num_counters,
+                               Scratch* out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ScratchEntry& e = g_scratch[{dev, reinterpret_cast<void*>(stream)}];
+    if (e.base && e.view.partial_bytes >= partial_bytes && e.view.num_counters >= num_counters) {
+        *out = e.view;
+        return CLOVE_OK;
+    }
+    const size_t pb = round_up_pow2(partial_bytes, (size_t)4 << 20);
+    const size_t nc = round_up_pow2(num_counters, 4096);
+    if (e.base) {
+        // in-flight work on this stream may still use the old buffer
+        if (hipStreamSynchronize(stream) != hipSuccess) return CLOVE_ERR_LAUNCH;
+        (void)hipFree(e.base);
+        e = ScratchEntry{};
+    }
+    void* base = nullptr;
+    if (hipMalloc(&base, pb + nc * sizeof(unsigned)) != hipSuccess) return CLOVE_ERR_OUT_OF_MEMORY;
+    unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(base) + pb);
+    hipLaunchKernelGGL(zero_u32, dim3(64), dim3(256), 0, stream, counters, nc);
+    if (hipGetLastError() != hipSuccess) {
+        (void)hipFree(base);
+        return CLOVE_ERR_LAUNCH;
+    }
+    e.base = base;
+    e.view.partials = static_cast<float*>(base);
+    e.view.partial_bytes = pb;
+    e.view.counters = counters;
+    e.view.num_counters = nc;
+    *out = e.view;
+    return CLOVE_OK;
+}
+
+}  // namespace clove
+
+using namespace clove;
+
+extern "C" {
+
+const char* clove_status_string(clove_status_t status) {
+    switch (status) {
+        case CLOVE_OK: return "CLOVE_OK";
+        case CLOVE_ERR_NULL_POINTER: return "CLOVE_ERR_NULL_POINTER: a required pointer is NULL";
+        case CLOVE_ERR_INVALID_DIM: return "CLOVE_ERR_INVALID_DIM: a dimension is negative or too large";
+        case CLOVE_ERR_INVALID_ARG: return "CLOVE_ERR_INVALID_ARG: invalid argument (odd K for INT4, mode, alignment)";
+        case CLOVE_ERR_ALIASING: return "CLOVE_ERR_ALIASING: output overlaps an input";
+        case CLOVE_ERR_OUT_OF_MEMORY: return "CLOVE_ERR_OUT_OF_MEMORY: scratch allocation failed";
+        case CLOVE_ERR_LAUNCH: return "CLOVE_ERR_LAUNCH: kernel launch failed";
+        case CLOVE_ERR_NO_DEVICE: return "CLOVE_ERR_NO_DEVICE: no usable HIP device";
+    }
+    return "CLOVE_ERR_UNKNOWN";
+}
+
+int clove_abi_version(void) { return kAbiVersion; }
+
+clove_status_t clove_gemm_fp16_batched(const void* A, const void* B, void* C, int batch, int M,
+                                       int N, int K, float alpha, float beta, void* stream) {
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (batch == 0 || M == 0 || N == 0) return CLOVE_OK;
+    if (!C || (K > 0 && (!A || !B))) return CLOVE_ERR_NULL_POINTER;
+    if (!aligned2(A) || !aligned2(B) || !aligned2(C)) return CLOVE_ERR_INVALID_ARG;
+    const size_t bc = (size_t)batch * M * N * 2;
+    if (overlaps(C, bc, A, (size_t)batch * M * K * 2) || overlaps(C, bc, B, (size_t)batch * K * N * 2))
+        return CLOVE_ERR_ALIASING;
+    if ((int64_t)batch * (int64_t)cdiv64(M, 32) * (int64_t)cdiv64(N, 128) > 0x3fffffff)
+        return CLOVE_ERR_INVALID_DIM;
+    return launch_gemm_fp16(static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B),
+                            static_cast<uint16_t*>(C), batch, M, N, K, alpha, beta,
+                            static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K,
+                               float alpha, float beta, void* stream) {
+    return clove_gemm_fp16_batched(A, B, C, 1, M, N, K, alpha, beta, stream);
+}
+
+static clove_status_t int8_common(Int8Args& a, void* stream) {
+    if (a.M < 0 || a.N < 0 || a.K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (a.M == 0 || a.N == 0) return CLOVE_OK;
+    if (!a.C || (a.K > 0 && (!a.A || !a.B))) return CLOVE_ERR_NULL_POINTER;
+    const size_t out_elt = a.out == Int8Out::kAcc32 ? 4 : 2;
+    if (a.out == Int8Out::kAcc32 ? (reinterpret_cast<uintptr_t>(a.C) & 3u) != 0 : !aligned2(a.C))
+        return CLOVE_ERR_INVALID_ARG;
+    const size_t bc = (size_t)a.M * a.N * out_elt;
+    if (overlaps(a.C, bc, a.A, (size_t)a.M * a.K) || overlaps(a.C, bc, a.B, (size_t)a.K * a.N))
+        return CLOVE_ERR_ALIASING;
+    if (a.out == Int8Out::kHalfRowCol) {
+        if (!a.sa || !a.sb) return CLOVE_ERR_NULL_POINTER;
+        if (!aligned2(a.sa) || !aligned2(a.sb)) return CLOVE_ERR_INVALID_ARG;
+        if (overlaps(a.C, bc, a.sa, (size_t)a.M * 2) || overlaps(a.C, bc, a.sb, (size_t)a.N * 2))
+            return CLOVE_ERR_ALIASING;
+    }
+    return launch_gemm_int8(a, static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_gemm_int8(const int8_t* A_q, const int8_t* B_q, void* C, int M, int N, int K,
+                               float A_scale, int8_t A_zero, float B_scale, int8_t B_zero,
+                               void* stream) {
+    Int8Args a;
+    a.A = A_q; a.B = B_q; a.C = C; a.M = M; a.N = N; a.K = K;
+    a.scale = A_scale * B_scale;  // combined in fp32 (src/kernels/gemm_int8.cu:40)
+    a.za = A_zero; a.zb = B_zero;
+    a.out = Int8Out::kHalfPerTensor;
+    return int8_common(a, stream);
+}
+
+clove_status_t clove_gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q, const void* A_scale,
+                                      const void* B_scale, void* C, int M, int N, int K,
+                                      int8_t A_zero, int8_t B_zero, void* stream) {
+    Int8Args a;
+    a.A = A_q; a.B = B_q; a.C = C; a.M = M; a.N = N; a.K = K;
+    a.sa = static_cast<const uint16_t*>(A_scale);
+    a.sb = static_cast<const uint16_t*>(B_scale);
+    a.za = A_zero; a.zb = B_zero;
+    a.out = Int8Out::kHalfRowCol;
+    return int8_common(a, stream);
+}
+
+clove_status_t clove_gemm_int8_acc32(const int8_t* A_q, const int8_t* B_q, int32_t* acc, int M,
+                                     int N, int K, int8_t A_zero, int8_t B_zero, void* stream) {
+    Int8Args a;
+    a.A = A_q; a.B = B_q; a.C = acc; a.M = M; a.N = N; a.K = K;
+    a.za = A_zero; a.zb = B_zero;
+    a.out = Int8Out::kAcc32;
+    return int8_common(a, stream);
+}
+
+clove_status_t clove_gemm_int4_ex(const uint8_t* A_q, const void* A_scale, const void* A_zero,
+                                  const uint8_t* B_q, const void* B_scale, const void* B_zero,
+                                  void* C, int M, int N, int K, clove_int4_mode_t mode,
+                                  void* stream) {
+    if (mode != CLOVE_INT4_GROUPWISE && mode != CLOVE_INT4_REFERENCE_LITERAL)
+        return CLOVE_ERR_INVALID_ARG;
+    if (M < 0 || N < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (K % 2 != 0) return CLOVE_ERR_INVALID_ARG;
+    if (M == 0 || N == 0) return CLOVE_OK;
+    const bool literal = mode == CLOVE_INT4_REFERENCE_LITERAL;
+    if (!C) return CLOVE_ERR_NULL_POINTER;
+    if (K > 0) {
+        if (!A_q || !A_scale || !B_scale) return CLOVE_ERR_NULL_POINTER;
+        if (!literal && (!A_zero || !B_zero || !B_q)) return CLOVE_ERR_NULL_POINTER;
+        if (literal && N >= 2 && !B_q) return CLOVE_ERR_NULL_POINTER;
+    }
+    if (!aligned2(C) || !aligned2(A_scale) || !aligned2(B_scale) || !aligned2(A_zero) ||
+        !aligned2(B_zero))
+        return CLOVE_ERR_INVALID_ARG;
+    const int64_t G = cdiv64(K, 128);
+    const size_t bc = (size_t)M * N * 2;
+    const size_t bstride = literal ? (size_t)(N / 2) : (size_t)((N + 1) / 2);
+    if (overlaps(C, bc, A_q, (size_t)M * (K / 2)) || overlaps(C, bc, B_q, (size_t)K * bstride) ||
+        overlaps(C, bc, A_scale, (size_t)M * G * 2) || overlaps(C, bc, B_scale, (size_t)G * N * 2) ||
+        (!literal && (overlaps(C, bc, A_zero, (size_t)M * G * 2) ||
+                      overlaps(C, bc, B_zero, (size_t)G * N * 2))))
+        return CLOVE_ERR_ALIASING;
+    Int4Args a;
+    a.A = A_q;
+    a.A_scale = static_cast<const uint16_t*>(A_scale);
+    a.A_zero = static_cast<const uint16_t*>(A_zero);
+    a.B = B_q;
+    a.B_scale = static_cast<const uint16_t*>(B_scale);
+    a.B_zero = static_cast<const uint16_t*>(B_zero);
+    a.C = static_cast<uint16_t*>(C);
+    a.M = M; a.N = N; a.K = K;
+    a.mode = mode;
+    return launch_gemm_int4(a, static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_gemm_int4(const uint8_t* A_q, const void* A_scale, const void* A_zero,
+                               const uint8_t* B_q, const void* B_scale, const void* B_zero,
+                               void* C, int M, int N, int K, void* stream) {
+    return clove_gemm_int4_ex(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M, N, K,
+                              CLOVE_INT4_GROUPWISE, stream);
+}
+
+clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q, const void* W_scale,
+                                const void* W_zero, void* Y, int T, int O, int K, float alpha,
+                                float beta, void* stream) {
+    if (T < 0 || O < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (K % 2 != 0) return CLOVE_ERR_INVALID_ARG;
+    if (T == 0 || O == 0) return CLOVE_OK;
+    if (!Y || (K > 0 && (!X || !W_q || !W_scale || !W_zero))) return CLOVE_ERR_NULL_POINTER;
+    if (!aligned2(X) || !aligned2(Y) || !aligned2(W_scale) || !aligned2(W_zero))
+        return CLOVE_ERR_INVALID_ARG;
+    const int64_t G = cdiv64(K, 128);
+    const size_t by = (size_t)T * O * 2;
+    if (overlaps(Y, by, X, (size_t)T * K * 2) || overlaps(Y, by, W_q, (size_t)O * (K / 2)) ||
+        overlaps(Y, by, W_scale, (size_t)O * G * 2) || overlaps(Y, by, W_zero, (size_t)O * G * 2))
+        return CLOVE_ERR_ALIASING;
+    W4A16Args a;
+    a.X = static_cast<const uint16_t*>(X);
+    a.W = W_q;
+    a.scale = static_cast<const uint16_t*>(W_scale);
+    a.zero = static_cast<const uint16_t*>(W_zero);
+    a.Y = static_cast<uint16_t*>(Y);
+    a.T = T; a.O = O; a.K = K;
+    a.alpha = alpha; a.beta = beta;
+    return launch_w4a16(a, static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_release_scratch(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    if (hipDeviceSynchronize() != hipSuccess) return CLOVE_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto it = g_scratch.begin(); it != g_scratch.end();) {
+        if (it->first.first == dev) {
+            (void)hipFree(it->second.base);
+            it = g_scratch.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    return CLOVE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+// Internal interface between the C ABI layer (capi.hip) and the kernel
+// launchers (gemm_*.hip).  Not installed; no reference counterpart.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "clove/gemm_c.h"
+
+namespace clove {
+
+// Per-(device, stream) scratch for split-K partials and completion counters.
+// Counters are zero between launches (each last-arriving workgroup resets its
+// own counter), so a launch may use them without clearing.
+struct Scratch {
+    float* partials = nullptr;
+    size_t partial_bytes = 0;
+    unsigned* counters = nullptr;
+    size_t num_counters = 0;
+};
+
+// Returns scratch with at least the requested capacity for `stream` on the
+// current device (implemented in capi.hip).
+clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t num_counters,
+                               Scratch* out);
+
+struct DeviceInfo {
+    int device = 0;
+    int num_cus = 256;
+};
+clove_status_t current_device_info(DeviceInfo* out);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch,
+                                int M, int N, int K, float alpha, float beta,
+                                hipStream_t stream);
+
+enum class Int8Out { kHalfPerTensor, kHalfRowCol, kAcc32 };
+
+struct Int8Args {
+    const int8_t* A = nullptr;
+    const int8_t* B = nullptr;
+    void* C = nullptr;  // uint16_t* (fp16) or int32_t* (kAcc32)
+    const uint16_t* sa = nullptr;  // [M] fp16 (kHalfRowCol)
+    const uint16_t* sb = nullptr;  // [N] fp16 (kHalfRowCol)
+    float scale = 1.0f;            // A_scale * B_scale (kHalfPerTensor)
+    int za = 0, zb = 0;
+    int M = 0, N = 0, K = 0;
+    Int8Out out = Int8Out::kHalfPerTensor;
+};
+clove_status_t launch_gemm_int8(const Int8Args& args, hipStream_t stream);
+
+struct Int4Args {
+    const uint8_t* A = nullptr;
+    const uint16_t* A_scale = nullptr;
+    const uint16_t* A_zero = nullptr;
+    const uint8_t* B = nullptr;
+    const uint16_t* B_scale = nullptr;
+    const uint16_t* B_zero = nullptr;
+    uint16_t* C = nullptr;
+    int M = 0, N = 0, K = 0;
+    clove_int4_mode_t mode = CLOVE_INT4_GROUPWISE;
+};
+clove_status_t launch_gemm_int4(const Int4Args& args, hipStream_t stream);
+
+struct W4A16Args {
+    const uint16_t* X = nullptr;
+    const uint8_t* W = nullptr;
+    const uint16_t* scale = nullptr;
+    const uint16_t* zero = nullptr;
+    uint16_t* Y = nullptr;
+    int T = 0, O = 0, K = 0;
+    float alpha = 1.0f, beta = 0.0f;
+};
+clove_status_t launch_w4a16(const W4A16Args& args, hipStream_t stream);
+
+inline clove_status_t check_launch() {
+    return hipGetLastError() == hipSuccess ? CLOVE_OK : CLOVE_ERR_LAUNCH;
+}
+
+}  // namespace clove

@@ -1,0 +1,101 @@
+"""Python mirror of the reference GEMM API (include/clove/kernels/gemm.cuh:41-101).
+
+Same function names, argument order and defaults as the reference's C++ API;
+buffers are torch tensors on a HIP device (or raw device addresses as int).
+Every call goes through the C ABI of libclove_gemm.so and is asynchronous on
+``stream`` (default: torch's current stream).  Where the reference prints the
+error and exits (include/clove/common.cuh:11-21), these raise CloveError.
+"""
+from __future__ import annotations
+
+from typing import Optional, Union
+
+from . import _lib
+
+INT4_GROUP_SIZE = 128  # include/clove/kernels/gemm.cuh:72
+
+Buffer = Union["torch.Tensor", int, None]  # noqa: F821
+
+
+def _ptr(x: Buffer) -> Optional[int]:
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if not x.is_cuda:
+        raise ValueError("clove GEMM buffers must live on the GPU")
+    if not x.is_contiguous():
+        raise ValueError("clove GEMM buffers must be contiguous row-major")
+    return x.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def gemm_fp16(A, B, C, M: int, N: int, K: int, alpha: float = 1.0, beta: float = 0.0,
+              stream=None) -> None:
+    """C = alpha * A @ B + beta * C (fp16, fp32 accumulate)."""
+    _lib.check(_lib.lib().clove_gemm_fp16(_ptr(A), _ptr(B), _ptr(C), M, N, K, alpha, beta,
+                                          _stream(stream)), "gemm_fp16")
+
+
+def gemm_fp16_batched(A, B, C, batch: int, M: int, N: int, K: int, alpha: float = 1.0,
+                      beta: float = 0.0, stream=None) -> None:
+    _lib.check(_lib.lib().clove_gemm_fp16_batched(_ptr(A), _ptr(B), _ptr(C), batch, M, N, K,
+                                                  alpha, beta, _stream(stream)),
+               "gemm_fp16_batched")
+
+
+def gemm_int8(A_q, B_q, C, M: int, N: int, K: int, A_scale: float, A_zero: int,
+              B_scale: float, B_zero: int, stream=None) -> None:
+    """C = fp16(float(sum (a - za)(b - zb)) * (A_scale * B_scale))."""
+    _lib.check(_lib.lib().clove_gemm_int8(_ptr(A_q), _ptr(B_q), _ptr(C), M, N, K, A_scale,
+                                          A_zero, B_scale, B_zero, _stream(stream)),
+               "gemm_int8")
+
+
+def gemm_int8_rowcol(A_q, B_q, A_scale, B_scale, C, M: int, N: int, K: int,
+                     A_zero: int = 0, B_zero: int = 0, stream=None) -> None:
+    _lib.check(_lib.lib().clove_gemm_int8_rowcol(_ptr(A_q), _ptr(B_q), _ptr(A_scale),
+                                                 _ptr(B_scale), _ptr(C), M, N, K, A_zero,
+                                                 B_zero, _stream(stream)), "gemm_int8_rowcol")
+
+
+def gemm_int8_acc32(A_q, B_q, acc, M: int, N: int, K: int, A_zero: int = 0, B_zero: int = 0,
+                    stream=None) -> None:
+    _lib.check(_lib.lib().clove_gemm_int8_acc32(_ptr(A_q), _ptr(B_q), _ptr(acc), M, N, K,
+                                                A_zero, B_zero, _stream(stream)),
+               "gemm_int8_acc32")
+
+
+def gemm_int4(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M: int, N: int, K: int,
+              stream=None) -> None:
+    """Group-wise W4A4 (group 128 along K); layouts as in include/clove/gemm_c.h."""
+    _lib.check(_lib.lib().clove_gemm_int4(_ptr(A_q), _ptr(A_scale), _ptr(A_zero), _ptr(B_q),
+                                          _ptr(B_scale), _ptr(B_zero), _ptr(C), M, N, K,
+                                          _stream(stream)), "gemm_int4")
+
+
+def gemm_int4_ex(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M: int, N: int, K: int,
+                 mode: int = _lib.CLOVE_INT4_GROUPWISE, stream=None) -> None:
+    _lib.check(_lib.lib().clove_gemm_int4_ex(_ptr(A_q), _ptr(A_scale), _ptr(A_zero),
+                                             _ptr(B_q), _ptr(B_scale), _ptr(B_zero), _ptr(C),
+                                             M, N, K, mode, _stream(stream)), "gemm_int4_ex")
+
+
+def gemm_w4a16(X, W_q, W_scale, W_zero, Y, T: int, O: int, K: int, alpha: float = 1.0,
+               beta: float = 0.0, stream=None) -> None:
+    """Y = alpha * X @ dequant(W)^T + beta * Y with group-128 INT4 weights."""
+    _lib.check(_lib.lib().clove_gemm_w4a16(_ptr(X), _ptr(W_q), _ptr(W_scale), _ptr(W_zero),
+                                           _ptr(Y), T, O, K, alpha, beta, _stream(stream)),
+               "gemm_w4a16")
+
+
+def release_scratch() -> None:
+    _lib.check(_lib.lib().clove_release_scratch(), "release_scratch")

@@ -1,0 +1,164 @@
+/*
+ * clove_gemm C ABI -- MI355X (gfx950) GEMM hot path of Clove Compute.
+ *
+ * Plain C: raw device pointers, int dimensions, a status code.  Every entry
+ * point is asynchronous on `stream` (a hipStream_t; NULL = the default stream),
+ * does not synchronise the host, and validates its arguments before touching
+ * the GPU.  Half-precision buffers are IEEE binary16 (passed as void*).
+ * All matrices are dense row-major.  Output buffers must not overlap inputs.
+ *
+ * Each declaration names the reference interface it replaces (paths relative
+ * to the Clove Compute source tree).  The C++ spellings with the reference's
+ * names, argument order and defaults live in <clove/gemm.h>.
+ *
+ * Scratch: split-K launches keep a per-(device, stream) scratch buffer that
+ * the library allocates on first use (hipMalloc) and keeps until
+ * clove_release_scratch() or process exit.  Calls on different streams never
+ * share scratch; calls on one stream are ordered by the stream.
+ */
+#ifndef CLOVE_GEMM_C_H
+#define CLOVE_GEMM_C_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum clove_status {
+    CLOVE_OK = 0,
+    CLOVE_ERR_NULL_POINTER = 1,   /* a required pointer is NULL */
+    CLOVE_ERR_INVALID_DIM = 2,    /* a dimension is negative */
+    CLOVE_ERR_INVALID_ARG = 3,    /* odd K for INT4, bad mode, misaligned half pointer */
+    CLOVE_ERR_ALIASING = 4,       /* the output overlaps an input */
+    CLOVE_ERR_OUT_OF_MEMORY = 5,  /* scratch allocation failed */
+    CLOVE_ERR_LAUNCH = 6,         /* the HIP runtime rejected a launch */
+    CLOVE_ERR_NO_DEVICE = 7       /* no usable HIP device */
+} clove_status_t;
+
+/* INT4 arithmetic selected by clove_gemm_int4_ex. */
+typedef enum clove_int4_mode {
+    /* per-128-group (q - zero) * scale on both operands, int32 partials per group
+     * (the layout and scales the reference API declares) */
+    CLOVE_INT4_GROUPWISE = 0,
+    /* the reference kernel's arithmetic: q - 8, zeros ignored, whole-K integer
+     * sum scaled by the last group's scales, B stride floor(N/2)
+     * (src/kernels/gemm_int4.cu:45-193) */
+    CLOVE_INT4_REFERENCE_LITERAL = 1
+} clove_int4_mode_t;
+
+/* include/clove/kernels/gemm.cuh:72 (INT4_GROUP_SIZE) */
+#define CLOVE_INT4_GROUP_SIZE 128
+
+/* Human-readable name of a status code (static storage). */
+const char* clove_status_string(clove_status_t status);
+
+/* ABI revision of this header; bumped on any signature change. */
+int clove_abi_version(void);
+
+/*
+ * C = alpha * A @ B + beta * C.  A [M,K], B [K,N], C [M,N], fp16; fp32
+ * accumulation and fp32 epilogue, fp16 round-to-nearest-even output.
+ * beta == 0 never reads C.  M == 0 or N == 0 is a no-op; K == 0 gives beta*C.
+ * Replaces clove::gemm_fp16 (include/clove/kernels/gemm.cuh:41-49,
+ * src/kernels/gemm_fp16.cu:277-305).
+ */
+clove_status_t clove_gemm_fp16(const void* A, const void* B, void* C,
+                               int M, int N, int K, float alpha, float beta,
+                               void* stream);
+
+/*
+ * Batched clove_gemm_fp16 with contiguous batches: A [batch,M,K],
+ * B [batch,K,N], C [batch,M,N].
+ * Replaces clove::gemm_fp16_batched (include/clove/kernels/gemm.cuh:93-101,
+ * src/kernels/gemm_fp16.cu:366-383).
+ */
+clove_status_t clove_gemm_fp16_batched(const void* A, const void* B, void* C,
+                                       int batch, int M, int N, int K,
+                                       float alpha, float beta, void* stream);
+
+/*
+ * W8A8 with per-tensor scale and zero point:
+ *   acc = sum_k (A_q[m,k] - A_zero) * (B_q[k,n] - B_zero)      (int32, exact)
+ *   C   = fp16( float(acc) * (A_scale * B_scale) )
+ * A_q [M,K], B_q [K,N] int8; C [M,N] fp16.
+ * Replaces clove::gemm_int8 (include/clove/kernels/gemm.cuh:57-65,
+ * src/kernels/gemm_int8.cu:119-137).
+ */
+clove_status_t clove_gemm_int8(const int8_t* A_q, const int8_t* B_q, void* C,
+                               int M, int N, int K,
+                               float A_scale, int8_t A_zero,
+                               float B_scale, int8_t B_zero, void* stream);
+
+/*
+ * W8A8 with fp16 per-row scales A_scale [M] (tokens) and per-column scales
+ * B_scale [N] (output channels): C = fp16(float(acc) * (A_scale[m]*B_scale[n])).
+ * With broadcast scales it equals clove_gemm_int8 bit for bit.  Extension of
+ * clove::gemm_int8 (include/clove/kernels/gemm.cuh:57-65), which is per-tensor.
+ */
+clove_status_t clove_gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q,
+                                      const void* A_scale, const void* B_scale,
+                                      void* C, int M, int N, int K,
+                                      int8_t A_zero, int8_t B_zero, void* stream);
+
+/*
+ * Test hook: the raw int32 accumulators [M,N] of the INT8 kernels (same kernels,
+ * integer epilogue).  No reference counterpart: it exposes the bit-exact
+ * accumulator the reference's gemm_int8_kernel keeps in registers
+ * (src/kernels/gemm_int8.cu:37, :87-96).
+ */
+clove_status_t clove_gemm_int8_acc32(const int8_t* A_q, const int8_t* B_q,
+                                     int32_t* acc, int M, int N, int K,
+                                     int8_t A_zero, int8_t B_zero, void* stream);
+
+/*
+ * Packed INT4 x INT4 GEMM, group-wise (CLOVE_INT4_GROUPWISE):
+ *   A_q [M, K/2]        two nibbles per byte, even k in the high nibble
+ *   A_scale, A_zero     [M, ceil(K/128)] fp16
+ *   B_q [K, ceil(N/2)]  two nibbles per byte along N, even n in the high nibble
+ *   B_scale, B_zero     [ceil(K/128), N] fp16
+ *   C [M,N] fp16 = sum_g A_scale[m,g]*B_scale[g,n] *
+ *                  sum_{k in g} (qA - zA[m,g]) * (qB - zB[g,n])
+ * Zero points are integer offsets stored as fp16 (non-integers round to nearest
+ * even).  K must be even.  For even N the byte layout is the reference's.
+ * Replaces clove::gemm_int4 (include/clove/kernels/gemm.cuh:77-87,
+ * src/kernels/gemm_int4.cu:195-216).
+ */
+clove_status_t clove_gemm_int4(const uint8_t* A_q, const void* A_scale,
+                               const void* A_zero, const uint8_t* B_q,
+                               const void* B_scale, const void* B_zero, void* C,
+                               int M, int N, int K, void* stream);
+
+/* clove_gemm_int4 with an explicit arithmetic mode (see clove_int4_mode_t).
+ * In CLOVE_INT4_REFERENCE_LITERAL mode B_q is [K, floor(N/2)] as in the
+ * reference and the zero pointers may be NULL (never read). */
+clove_status_t clove_gemm_int4_ex(const uint8_t* A_q, const void* A_scale,
+                                  const void* A_zero, const uint8_t* B_q,
+                                  const void* B_scale, const void* B_zero,
+                                  void* C, int M, int N, int K,
+                                  clove_int4_mode_t mode, void* stream);
+
+/*
+ * W4A16 linear layer: fp16 activations x group-128 INT4 weights.
+ *   Y[t,o] = alpha * sum_k X[t,k] * (qW(o,k) - W_zero[o,g]) * W_scale[o,g]
+ *            + beta * Y[t,o]
+ * X [T,K] fp16, W_q [O, K/2] (gemm_int4's A layout), W_scale/W_zero [O, K/128]
+ * fp16, Y [T,O] fp16.  beta = 1 is the residual add of the reference's o_proj
+ * and down_proj (src/runtime/inference.cu:165-168, :191-194).  K even.
+ * No reference entry point takes fp16 activations with INT4 weights; this is
+ * the linear-layer call (src/runtime/inference.cu:139-194) on INT4 weights.
+ */
+clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q,
+                                const void* W_scale, const void* W_zero, void* Y,
+                                int T, int O, int K, float alpha, float beta,
+                                void* stream);
+
+/* Frees the scratch buffers held for the current device (all streams).
+ * Synchronises the device first.  No reference counterpart. */
+clove_status_t clove_release_scratch(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLOVE_GEMM_C_H */

@@ -1,0 +1,163 @@
+"""GPU parity of clove_gemm_fp16 / clove_gemm_fp16_batched against the oracle.
+
+Shapes: the reference test's six cases (tests/test_gemm.cu:99-243), the
+512^3 U[-1,1] workload and the LLM shapes with N(0,1) activations x N(0,0.02)
+weights, ragged and unaligned shapes, and batched calls.  Bit-exact where the
+mathematics fixes the answer (small-integer inputs); otherwise within
+|got - ref| <= 1e-2 * max(|ref|, 1e-2 * rms(ref)) of the float64 oracle.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import empty_f16, f16bits, rng, to_dev, to_host, within_tol
+
+pytestmark = pytest.mark.gpu
+
+
+def _cg():
+    import clove_compute_amd as cg
+    return cg
+
+
+def run_fp16(A, B, C0=None, alpha=1.0, beta=0.0):
+    import torch
+    M, K = A.shape
+    N = B.shape[1]
+    dA, dB = to_dev(A), to_dev(B)
+    dC = to_dev(C0) if C0 is not None else empty_f16(M, N, fill=float("nan"))
+    _cg().gemm_fp16(dA, dB, dC, M, N, K, alpha, beta)
+    torch.cuda.synchronize()
+    return to_host(dC)
+
+
+def check_rows(A, B, C, rows, C0=None, alpha=1.0, beta=0.0):
+    ref = oracle.gemm_fp16_f64(A[rows], B, None if C0 is None else C0[rows], alpha, beta)
+    ok, rep = within_tol(C[rows], ref)
+    assert ok, rep
+    assert rep["ref_rule_failures"] == 0, rep
+
+
+# the reference's own FP16 cases (tests/test_gemm.cu:99-219), inputs U[-0.1, 0.1)
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (256, 256, 256), (1024, 1024, 1024),
+                                   (128, 4096, 4096), (1, 4096, 4096)])
+def test_reference_cases(M, N, K):
+    g = rng("ref", M, N, K)
+    A = g.uniform(-0.1, 0.1, (M, K)).astype(np.float16)
+    B = g.uniform(-0.1, 0.1, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, min(M, 24))]))
+    check_rows(A, B, C, rows)
+
+
+def test_reference_alpha_beta():
+    # tests/test_gemm.cu:221-243 (smoke-only there); checked here
+    g = rng("alpha_beta")
+    M = N = K = 128
+    A = g.uniform(-0.1, 0.1, (M, K)).astype(np.float16)
+    B = g.uniform(-0.1, 0.1, (K, N)).astype(np.float16)
+    C0 = g.uniform(-0.1, 0.1, (M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=0.5, beta=0.25)
+    check_rows(A, B, C, np.arange(M), C0, 0.5, 0.25)
+
+
+def test_512_cubed_uniform_full():
+    # 512^3, A and B ~ U[-1, 1]: every element against the oracle
+    g = rng("cfg1")
+    A = g.uniform(-1, 1, (512, 512)).astype(np.float16)
+    B = g.uniform(-1, 1, (512, 512)).astype(np.float16)
+    C = run_fp16(A, B)
+    check_rows(A, B, C, np.arange(512))
+    # the naive-arithmetic restatement agrees to a few fp16 ulps as well
+    Co = oracle.gemm_fp16(A, B)
+    assert np.max(np.abs(C.astype(np.float64) - Co.astype(np.float64))) < 4e-3 * 512 ** 0.5
+
+
+@pytest.mark.parametrize("M", [1, 32, 128, 4096])
+def test_llm_shapes(M):
+    N = K = 4096
+    g = rng("cfg2", M)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.02).astype(np.float16)
+    C = run_fp16(A, B)
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, min(M, 16))]))
+    check_rows(A, B, C, rows)
+    assert np.all(np.isfinite(C.astype(np.float32)))
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 512), (1, 4096, 4096), (7, 96, 300), (4096, 4096, 4096)])
+def test_small_integer_inputs_bit_exact(M, N, K):
+    # |a|,|b| <= 2: every fp32 partial sum is an exact integer, |C| < 2048 for
+    # these sizes with overwhelming probability, so C is exact in any order
+    g = rng("int", M, N, K)
+    A = g.integers(-2, 3, (M, K)).astype(np.float16)
+    B = g.integers(-2, 3, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(f16bits(C), f16bits(exact.astype(np.float16)))
+
+
+@pytest.mark.parametrize("M,N,K", [(77, 45, 131), (3, 17, 33), (130, 257, 96), (33, 8, 8),
+                                   (5, 4096, 64), (1, 7, 1), (300, 129, 1000)])
+def test_ragged_and_unaligned(M, N, K):
+    g = rng("ragged", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = g.standard_normal((K, N)).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=1.5, beta=-0.75)
+    check_rows(A, B, C, np.arange(M), C0, 1.5, -0.75)
+
+
+def test_k_zero_and_empty():
+    import torch
+    cg = _cg()
+    C0 = np.arange(12, dtype=np.float16).reshape(3, 4)
+    dC = to_dev(C0)
+    dA = empty_f16(3, 1)
+    dB = empty_f16(1, 4)
+    cg.gemm_fp16(dA, dB, dC, 3, 4, 0, 1.0, 0.5)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_host(dC), (C0.astype(np.float32) * 0.5).astype(np.float16))
+    cg.gemm_fp16(dA, dB, dC, 0, 4, 5)  # no-op
+    cg.gemm_fp16(dA, dB, dC, 3, 0, 5)  # no-op
+
+
+def test_beta_zero_ignores_nan_in_c():
+    g = rng("nanc")
+    A = g.integers(-3, 4, (64, 64)).astype(np.float16)
+    B = g.integers(-3, 4, (64, 128)).astype(np.float16)
+    C = run_fp16(A, B, np.full((64, 128), np.nan, np.float16), 1.0, 0.0)
+    assert np.array_equal(f16bits(C), f16bits((A.astype(np.float64) @ B.astype(np.float64)).astype(np.float16)))
+
+
+@pytest.mark.parametrize("batch,M,N,K", [(3, 64, 96, 80), (4, 1, 256, 512), (2, 300, 200, 64)])
+def test_batched(batch, M, N, K):
+    import torch
+    g = rng("batched", batch, M, N, K)
+    A = g.standard_normal((batch, M, K)).astype(np.float16)
+    B = g.standard_normal((batch, K, N)).astype(np.float16)
+    C0 = g.standard_normal((batch, M, N)).astype(np.float16)
+    dC = to_dev(C0)
+    _cg().gemm_fp16_batched(to_dev(A), to_dev(B), dC, batch, M, N, K, 0.5, 1.0)
+    torch.cuda.synchronize()
+    C = to_host(dC)
+    for b in range(batch):
+        ref = oracle.gemm_fp16_f64(A[b], B[b], C0[b], 0.5, 1.0)
+        ok, rep = within_tol(C[b], ref)
+        assert ok, (b, rep)
+
+
+def test_repeat_calls_deterministic_split_k():
+    # split-K shapes reduce in a fixed order: repeated calls are bit-identical
+    import torch
+    g = rng("det")
+    M, N, K = 32, 4096, 4096
+    A = to_dev(g.standard_normal((M, K)).astype(np.float16))
+    B = to_dev((g.standard_normal((K, N)) * 0.02).astype(np.float16))
+    outs = []
+    for _ in range(3):
+        C = empty_f16(M, N)
+        _cg().gemm_fp16(A, B, C, M, N, K)
+        torch.cuda.synchronize()
+        outs.append(f16bits(to_host(C)))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
