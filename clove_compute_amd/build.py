@@ -24,6 +24,9 @@ ARCH = "gfx950"
 CFLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-munsafe-fp-atomics",
+    # every fused multiply-add is written as fmaf(); no implicit contraction
+    # (which would also fuse fp32 multiplies with the fp16 narrowing)
+    "-ffp-contract=off",
     # keep hipcc from emitting packed fp32 VALU ops
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",

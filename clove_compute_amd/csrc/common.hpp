@@ -39,7 +39,12 @@ __device__ __forceinline__ To bitcast(const From& v) {
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(bitcast<_Float16>(h));
 }
+// The empty asm pins f as an fp32 register value: without it the backend folds
+// a preceding fp32 multiply into the narrowing (v_fma_mixlo_f16, one rounding
+// of the exact product), while the reference rounds to fp32 first and then to
+// fp16 (float result = ...; __float2half(result)).
 __device__ __forceinline__ uint16_t f2h(float f) {
+    asm("" : "+v"(f));
     return bitcast<uint16_t>(static_cast<_Float16>(f));
 }
 __device__ __forceinline__ unsigned pack2h(float lo, float hi) {
@@ -47,29 +52,37 @@ __device__ __forceinline__ unsigned pack2h(float lo, float hi) {
 }
 
 // ---------------------------------------------------------------------------
-// split-K completion: the last workgroup of a tile to arrive reduces the
-// partials.  Release/acquire at agent scope make the fp32 partials written by
-// workgroups on other XCDs visible (agent-scope fences write back / invalidate
-// the per-XCD L2 for coarse-grained memory).
+// split-K publication without whole-cache maintenance.
+//
+// Partials are written with agent-scope relaxed atomic stores (global_store
+// ... sc1: written through past the per-XCD L2) and read back with agent-scope
+// relaxed atomic loads (sc1: served from the device-coherent level), so no
+// L2 writeback/invalidate (what __threadfence() costs on a multi-XCD part) is
+// needed.  Each thread waits for its own stores to be acknowledged before the
+// workgroup barrier; thread 0 then bumps the tile's counter.  The workgroup
+// that observes count == nsplit-1 is the last one and reduces.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ bool splitk_arrive_is_last(unsigned* counter, unsigned nsplit,
                                                       int* lds_flag) {
-    __threadfence();  // release this workgroup's partial stores
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's coherent stores are acknowledged
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        int last = (prev == nsplit - 1) ? 1 : 0;
-        if (last) {
-            // reset for the next launch on this scratch (stream order makes it safe)
-            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        const unsigned prev =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = (prev == nsplit - 1) ? 1 : 0;
+        // the last arriver re-arms the counter for the next launch on this scratch
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *lds_flag = last;
     }
     __syncthreads();
-    const bool last = *lds_flag != 0;
-    if (last) __threadfence();  // acquire the other workgroups' partials
-    return last;
+    return *lds_flag != 0;
 }
 
 }  // namespace hw

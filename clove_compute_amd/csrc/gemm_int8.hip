@@ -1,0 +1,469 @@
+// INT8 (W8A8) GEMM for gfx950.
+//
+//   acc[m,n] = sum_k (A_q[m,k] - za) * (B_q[k,n] - zb)      int32, exact
+//   C[m,n]   = fp16(float(acc) * scale)   scale = A_scale*B_scale, or sa[m]*sb[n]
+//
+// Replaces the reference's gemm_int8 (src/kernels/gemm_int8.cu:16-137; the
+// per-element formula is :37-40, :87-96, :113-114).
+//
+//  * int8_mfma -- v_mfma_i32_32x32x32_i8 on the raw operands.  Zero points are
+//    applied exactly in the epilogue with the identity
+//        sum (a-za)(b-zb) = sum ab - zb*rowsum(A) - za*colsum(B) + K*za*zb
+//    (int32 wrap-around arithmetic, exact whenever the true value fits int32),
+//    the row/column sums coming from a small pre-pass when a zero is non-zero.
+//    B [K,N] is N-contiguous: each thread transposes 4 K rows x 16 columns of
+//    bytes in registers (v_perm) on the way to LDS.
+//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads, int32 MADs on
+//    the VALU with the zero points subtracted directly, split-K over workgroups.
+#include "common.hpp"
+#include "dispatch.hpp"
+#include "mfma_gemm.hpp"
+
+namespace clove {
+namespace i8 {
+
+using namespace hw;
+
+struct I8Params {
+    const int8_t* A;
+    const int8_t* B;
+    void* C;
+    const uint16_t* sa;
+    const uint16_t* sb;
+    const int* rowsum;  // [M] sum_k A (only when zb != 0)
+    const int* colsum;  // [N] sum_k B (only when za != 0)
+    float scale;
+    int za, zb;
+    int M, N, K;
+    int tiles_m, tiles_n, nsplit, k_per_split;
+    float* ws;
+    unsigned* counters;
+};
+
+template <int OUT>
+__device__ __forceinline__ void int8_store(const I8Params& p, int m, int n, int acc) {
+    if constexpr (OUT == (int)Int8Out::kAcc32) {
+        static_cast<int*>(p.C)[(int64_t)m * p.N + n] = acc;
+    } else {
+        float s;
+        if constexpr (OUT == (int)Int8Out::kHalfRowCol) s = h2f(p.sa[m]) * h2f(p.sb[n]);
+        else s = p.scale;
+        static_cast<uint16_t*>(p.C)[(int64_t)m * p.N + n] = f2h(static_cast<float>(acc) * s);
+    }
+}
+
+// exact zero-point correction, int32 wrap-around arithmetic
+__device__ __forceinline__ int zero_correct(const I8Params& p, int acc, int m, int n) {
+    unsigned r = (unsigned)acc;
+    if (p.zb != 0) r -= (unsigned)p.zb * (unsigned)p.rowsum[m];
+    if (p.za != 0) r -= (unsigned)p.za * (unsigned)p.colsum[n];
+    r += (unsigned)p.K * (unsigned)p.za * (unsigned)p.zb;
+    return (int)r;
+}
+
+// ---------------------------------------------------------------------------
+// pre-pass: row sums of A (one wave per row) and column sums of B
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) int8_rowsum(const int8_t* A, int M, int K, int* out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    int s = 0;
+    for (int k = lane; k < K; k += 64) s += A[(int64_t)row * K + k];
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) out[row] = s;
+}
+
+__global__ void __launch_bounds__(256) int8_colsum(const int8_t* B, int N, int K, int* out) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= N) return;
+    int s = 0;
+    for (int k = 0; k < K; ++k) s += B[(int64_t)k * N + n];
+    out[n] = s;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA tile kernel
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WGM, int WGN, int OUT, bool ALIGNED>
+__global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
+    constexpr int NT = WGM * WGN * 64;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr int LDK = BK + 16;  // bytes; 16-byte pad
+    static_assert(BK % 32 == 0 && WTM % 32 == 0 && WTN % 32 == 0, "tile");
+    constexpr int A_CH = BM * BK / 16;              // 16-byte chunks of A
+    constexpr int LA = (A_CH + NT - 1) / NT;
+    constexpr int B_BLK = (BK / 4) * (BN / 16);     // 4 K rows x 16 columns
+    constexpr int LB = (B_BLK + NT - 1) / NT;
+
+    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * LDK];
+    __shared__ int s_last;
+
+    mg::Params tp{};
+    tp.tiles_m = p.tiles_m; tp.tiles_n = p.tiles_n; tp.nsplit = p.nsplit;
+    const mg::TileCoord tc = mg::decode_tile(tp);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = tc.tm * BM, n0 = tc.tn * BN;
+    const int M = p.M, N = p.N, K = p.K;
+    const int kbeg = tc.split * p.k_per_split;
+    const int kend = min(K, kbeg + p.k_per_split);
+    const int ktiles = kend > kbeg ? cdiv(kend - kbeg, BK) : 0;
+
+    unsigned ra[LA][4];
+    unsigned rb[LB][4][4];
+
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const int c = tid + i * NT;
+            const int row = c / (BK / 16), kc = (c % (BK / 16)) * 16;
+            const int gm = m0 + row, gk = k0 + kc;
+            const bool in = (A_CH % NT == 0 || c < A_CH) && gm < M;
+            if constexpr (ALIGNED) {
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (in && gk < kend) v = *reinterpret_cast<const u32x4*>(p.A + (int64_t)gm * K + gk);
+                ra[i][0] = v.x; ra[i][1] = v.y; ra[i][2] = v.z; ra[i][3] = v.w;
+            } else {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    unsigned w = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int k = gk + 4 * d + e;
+                        const unsigned b = (in && k < kend) ? (uint8_t)p.A[(int64_t)gm * K + k] : 0u;
+                        w |= b << (8 * e);
+                    }
+                    ra[i][d] = w;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int b = tid + i * NT;
+            const bool bin = B_BLK % NT == 0 || b < B_BLK;
+            const int kb = b % (BK / 4), nb = b / (BK / 4);
+            const int gn = n0 + nb * 16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int gk = k0 + kb * 4 + r;
+                if constexpr (ALIGNED) {
+                    u32x4 v = {0u, 0u, 0u, 0u};
+                    if (bin && gk < kend && gn < N) v = *reinterpret_cast<const u32x4*>(p.B + (int64_t)gk * N + gn);
+                    rb[i][r][0] = v.x; rb[i][r][1] = v.y; rb[i][r][2] = v.z; rb[i][r][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        unsigned w = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int n = gn + 4 * d + e;
+                            const unsigned bb = (bin && gk < kend && n < N) ? (uint8_t)p.B[(int64_t)gk * N + n] : 0u;
+                            w |= bb << (8 * e);
+                        }
+                        rb[i][r][d] = w;
+                    }
+                }
+            }
+        }
+    };
+
+    auto store = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const int c = tid + i * NT;
+            if (A_CH % NT != 0 && c >= A_CH) continue;
+            const int row = c / (BK / 16), kc = (c % (BK / 16)) * 16;
+            *reinterpret_cast<u32x4*>(&sA[st][row * LDK + kc]) = u32x4{ra[i][0], ra[i][1], ra[i][2], ra[i][3]};
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const int b = tid + i * NT;
+            if (B_BLK % NT != 0 && b >= B_BLK) continue;
+            const int kb = b % (BK / 4), nb = b / (BK / 4);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                // 4x4 byte transpose of rows r=0..3, dword d -> columns 4d..4d+3
+                const unsigned t0 = __builtin_amdgcn_perm(rb[i][1][d], rb[i][0][d], 0x05010400u);
+                const unsigned t1 = __builtin_amdgcn_perm(rb[i][1][d], rb[i][0][d], 0x07030602u);
+                const unsigned t2 = __builtin_amdgcn_perm(rb[i][3][d], rb[i][2][d], 0x05010400u);
+                const unsigned t3 = __builtin_amdgcn_perm(rb[i][3][d], rb[i][2][d], 0x07030602u);
+                const unsigned c0 = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+                const unsigned c1 = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+                const unsigned c2 = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+                const unsigned c3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+                int8_t* dst = &sB[st][(nb * 16 + 4 * d) * LDK + kb * 4];
+                *reinterpret_cast<unsigned*>(dst) = c0;
+                *reinterpret_cast<unsigned*>(dst + LDK) = c1;
+                *reinterpret_cast<unsigned*>(dst + 2 * LDK) = c2;
+                *reinterpret_cast<unsigned*>(dst + 3 * LDK) = c3;
+            }
+        }
+    };
+
+    i32x16 acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    if (ktiles > 0) {
+        load(kbeg);
+        store(0);
+        __syncthreads();
+    }
+    const int lrow = lane & 31, lk = (lane >> 5) * 16;
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int st = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load(kbeg + (kt + 1) * BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            i32x4 bf[FN], af[FM];
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+                bf[i] = *reinterpret_cast<const i32x4*>(&sB[st][(wn * WTN + i * 32 + lrow) * LDK + kk + lk]);
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+                af[j] = *reinterpret_cast<const i32x4*>(&sA[st][(wm * WTM + j * 32 + lrow) * LDK + kk + lk]);
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[i], af[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) store(st ^ 1);
+        __syncthreads();
+    }
+
+    if (p.nsplit > 1) {
+        const int tile_id = tc.tm * p.tiles_n + tc.tn;
+        float* ws_tile = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
+        float* mine = ws_tile + (int64_t)tc.split * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    store_coherent(&mine[((i * FM + j) * 16 + r) * NT + tid], __int_as_float(acc[i][j][r]));
+        if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+        for (int s = 0; s < p.nsplit; ++s) {
+            const float* part = ws_tile + (int64_t)s * (BM * BN);
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        acc[i][j][r] += __float_as_int(load_coherent(&part[((i * FM + j) * 16 + r) * NT + tid]));
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int gm = m0 + wm * WTM + j * 32 + lrow;
+            if (gm >= M) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int gn = n0 + wn * WTN + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (gn < N) int8_store<OUT>(p, gm, gn, zero_correct(p, acc[i][j][r], gm, gn));
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV (M <= 4): 256 threads = 16 column lanes x 16 K lanes; a column lane
+// owns 16 consecutive columns (one 16-byte load per K row).
+// ---------------------------------------------------------------------------
+constexpr int IV_COLS = 256;
+constexpr int IV_KL = 16;
+constexpr int IV_UNROLL = 8;
+
+template <int MM, int OUT>
+__global__ void __launch_bounds__(256) int8_gemv(I8Params p, int col_blocks) {
+    __shared__ int red[IV_KL][MM][IV_COLS];
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    const int cl = tid & 15, kl = tid >> 4;
+    const int split = blockIdx.x % p.nsplit;
+    const int cb = blockIdx.x / p.nsplit;
+    const int M = p.M, N = p.N, K = p.K;
+    const int n = cb * IV_COLS + cl * 16;
+    const bool col_ok = n < N;
+    const int kbeg = split * p.k_per_split;
+    const int kend = min(K, kbeg + p.k_per_split);
+
+    int acc[MM][16];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[m][e] = 0;
+
+    for (int k = kbeg + kl; k < kend; k += IV_KL * IV_UNROLL) {
+        u32x4 bv[IV_UNROLL];
+#pragma unroll
+        for (int u = 0; u < IV_UNROLL; ++u) {
+            const int kk = k + u * IV_KL;
+            bv[u] = (col_ok && kk < kend)
+                        ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)kk * N + n))
+                        : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < IV_UNROLL; ++u) {
+            const int kk = k + u * IV_KL;
+            if (kk >= kend) break;
+            int bvals[16];
+            const unsigned w[4] = {bv[u].x, bv[u].y, bv[u].z, bv[u].w};
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                bvals[e] = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                const int a = (m < M) ? (int)p.A[(int64_t)m * K + kk] - p.za : 0;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[m][e] += a * bvals[e];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) red[kl][m][cl * 16 + e] = acc[m][e];
+    __syncthreads();
+    const int col = tid;
+    const int gn = cb * IV_COLS + col;
+    int sum[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        int s = 0;
+#pragma unroll
+        for (int q = 0; q < IV_KL; ++q) s += red[q][m][col];
+        sum[m] = s;
+    }
+    if (p.nsplit > 1) {
+        float* ws_tile = p.ws + (int64_t)cb * p.nsplit * (MM * IV_COLS);
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+            store_coherent(&ws_tile[(int64_t)split * MM * IV_COLS + m * IV_COLS + col], __int_as_float(sum[m]));
+        if (!splitk_arrive_is_last(&p.counters[cb], (unsigned)p.nsplit, &s_last)) return;
+#pragma unroll
+        for (int m = 0; m < MM; ++m) sum[m] = 0;
+        for (int s = 0; s < p.nsplit; ++s)
+#pragma unroll
+            for (int m = 0; m < MM; ++m)
+                sum[m] += __float_as_int(load_coherent(&ws_tile[(int64_t)s * MM * IV_COLS + m * IV_COLS + col]));
+    }
+    if (gn < N) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+            if (m < M) int8_store<OUT>(p, m, gn, sum[m]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int OUT>
+clove_status_t run_gemv(I8Params p, int cus, hipStream_t stream) {
+    const int col_blocks = cdiv(p.N, IV_COLS);
+    const int want = cdiv(4 * cus, col_blocks);
+    const int maxs = max(1, p.K / 64);
+    const int ns = max(1, min(want, maxs));
+    const int kps = cdiv(cdiv(p.K, ns), 16) * 16;
+    p.nsplit = cdiv(p.K, kps);
+    p.k_per_split = kps;
+    if (p.nsplit > 1) {
+        Scratch s;
+        const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
+        clove_status_t st = acquire_scratch(stream, (size_t)col_blocks * p.nsplit * mm * IV_COLS * 4,
+                                            (size_t)col_blocks, &s);
+        if (st != CLOVE_OK) return st;
+        p.ws = s.partials;
+        p.counters = s.counters;
+    }
+    const dim3 grid(col_blocks * p.nsplit);
+    if (p.M == 1) hipLaunchKernelGGL((int8_gemv<1, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
+    else if (p.M == 2) hipLaunchKernelGGL((int8_gemv<2, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
+    else hipLaunchKernelGGL((int8_gemv<4, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
+    return check_launch();
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int OUT, bool ALIGNED>
+clove_status_t run_mfma(I8Params p, int cus, hipStream_t stream) {
+    p.tiles_m = cdiv(p.M, BM);
+    p.tiles_n = cdiv(p.N, BN);
+    const int tiles = p.tiles_m * p.tiles_n;
+    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, BK, 2 * cus, 2);
+    p.nsplit = sp.nsplit;
+    p.k_per_split = sp.k_per_split;
+    const bool sums = (p.za != 0 || p.zb != 0) && p.K > 0;
+    const size_t part = p.nsplit > 1 ? (size_t)tiles * p.nsplit * BM * BN * 4 : 0;
+    const size_t aux = sums ? ((size_t)p.M + p.N) * sizeof(int) : 0;
+    if (part + aux > 0) {
+        // one scratch request: split-K partials first, then the zero-point sums
+        Scratch s;
+        clove_status_t st = acquire_scratch(stream, part + aux, (size_t)tiles, &s);
+        if (st != CLOVE_OK) return st;
+        p.ws = s.partials;
+        p.counters = s.counters;
+        if (sums) {
+            int* rs = reinterpret_cast<int*>(reinterpret_cast<char*>(s.partials) + part);
+            int* cs = rs + p.M;
+            hipLaunchKernelGGL(int8_rowsum, dim3(cdiv(p.M, 4)), dim3(256), 0, stream, p.A, p.M, p.K, rs);
+            hipLaunchKernelGGL(int8_colsum, dim3(cdiv(p.N, 256)), dim3(256), 0, stream, p.B, p.N, p.K, cs);
+            p.rowsum = rs;
+            p.colsum = cs;
+        }
+    }
+    hipLaunchKernelGGL((int8_mfma<BM, BN, BK, WGM, WGN, OUT, ALIGNED>), dim3(tiles * p.nsplit),
+                       dim3(WGM * WGN * 64), 0, stream, p);
+    return check_launch();
+}
+
+template <int OUT>
+clove_status_t dispatch(I8Params p, bool aligned, int cus, hipStream_t stream) {
+    if (aligned && p.M <= 4 && p.K > 0) return run_gemv<OUT>(p, cus, stream);
+    if (!aligned) return run_mfma<64, 64, 64, 2, 2, OUT, false>(p, cus, stream);
+    if (p.M <= 64) return run_mfma<64, 128, 128, 2, 2, OUT, true>(p, cus, stream);
+    if ((int64_t)cdiv(p.M, 256) * cdiv(p.N, 256) >= cus / 2)
+        return run_mfma<256, 256, 64, 2, 2, OUT, true>(p, cus, stream);
+    return run_mfma<128, 128, 128, 2, 2, OUT, true>(p, cus, stream);
+}
+
+}  // namespace
+}  // namespace i8
+
+clove_status_t launch_gemm_int8(const Int8Args& a, hipStream_t stream) {
+    using namespace i8;
+    DeviceInfo dev;
+    clove_status_t st = current_device_info(&dev);
+    if (st != CLOVE_OK) return st;
+    I8Params p{};
+    p.A = a.A; p.B = a.B; p.C = a.C; p.sa = a.sa; p.sb = a.sb;
+    p.scale = a.scale; p.za = a.za; p.zb = a.zb;
+    p.M = a.M; p.N = a.N; p.K = a.K;
+    const bool aligned = aligned16(a.A) && aligned16(a.B) && (a.K % 16 == 0) && (a.N % 16 == 0);
+    switch (a.out) {
+        case Int8Out::kHalfPerTensor: return dispatch<(int)Int8Out::kHalfPerTensor>(p, aligned, dev.num_cus, stream);
+        case Int8Out::kHalfRowCol: return dispatch<(int)Int8Out::kHalfRowCol>(p, aligned, dev.num_cus, stream);
+        case Int8Out::kAcc32: return dispatch<(int)Int8Out::kAcc32>(p, aligned, dev.num_cus, stream);
+    }
+    return CLOVE_ERR_INVALID_ARG;
+}
+
+}  // namespace clove

@@ -1,0 +1,124 @@
+"""GPU parity of clove_gemm_int4 / clove_gemm_int4_ex against the oracle.
+
+Group-wise mode: within |got - ref| <= 1e-2 * max(|ref|, 1e-2 * rms(ref)) of
+the float64 oracle, and bit-exact on power-of-two-scale cases where every
+step is exact.  Reference-literal mode: bit-exact (integer sum, then the
+reference's (acc * a_s) * b_s, src/kernels/gemm_int4.cu:185-190).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from clove_compute_amd import quant
+from tests._util import empty_f16, f16bits, rng, to_dev, to_host, within_tol
+
+pytestmark = pytest.mark.gpu
+
+LIT = 1
+
+
+def _cg():
+    import clove_compute_amd as cg
+    return cg
+
+
+def make_case(M, N, K, key, pow2=False, small=False):
+    g = rng("i4", M, N, K, key)
+    G = (K + 127) // 128
+    if small:
+        qA = g.integers(7, 10, (M, K))
+        qB = g.integers(7, 10, (K, N))
+    else:
+        qA = g.integers(0, 16, (M, K))
+        qB = g.integers(0, 16, (K, N))
+    A_q = quant.pack_rows(qA)
+    B_q = quant.pack_cols(qB)
+    if pow2:
+        sA = (2.0 ** -g.integers(0, 3, (M, G))).astype(np.float16)
+        sB = (2.0 ** -g.integers(0, 3, (G, N))).astype(np.float16)
+        zA = np.full((M, G), 8, np.float16)
+        zB = np.full((G, N), 8, np.float16)
+    else:
+        sA = g.uniform(0.001, 0.02, (M, G)).astype(np.float16)
+        sB = g.uniform(0.001, 0.02, (G, N)).astype(np.float16)
+        zA = g.integers(0, 16, (M, G)).astype(np.float16)
+        zB = g.integers(0, 16, (G, N)).astype(np.float16)
+    return A_q, sA, zA, B_q, sB, zB
+
+
+def run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K, mode=0):
+    import torch
+    C = empty_f16(M, N, fill=float("nan"))
+    _cg().gemm_int4_ex(to_dev(A_q), to_dev(sA), None if zA is None else to_dev(zA),
+                       None if B_q is None else to_dev(B_q), to_dev(sB),
+                       None if zB is None else to_dev(zB), C, M, N, K, mode)
+    torch.cuda.synchronize()
+    return to_host(C)
+
+
+@pytest.mark.parametrize("M,K", [(11008, 4096), (4096, 11008)])
+@pytest.mark.parametrize("N", [1, 16, 128])
+def test_config4_groupwise(M, N, K):
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "cfg4")
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    g = rng("rows", M, N, K)
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 24)]))
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
+    ok, rep = within_tol(C[rows], ref)
+    assert ok, rep
+    assert np.all(np.isfinite(C.astype(np.float32)))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 1, 4096), (260, 8, 2048), (100, 16, 1024), (130, 128, 512),
+                                   (64, 3, 640)])
+def test_groupwise_pow2_bit_exact(M, N, K):
+    # power-of-two scales, values q-z in [-1, 1]: every fp32/fp16 step is exact
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2", pow2=True, small=True)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    Cr, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))
+
+
+@pytest.mark.parametrize("M,N,K", [(77, 5, 200), (33, 17, 96), (65, 40, 330), (9, 1, 64), (130, 7, 4096)])
+def test_groupwise_ragged(M, N, K):
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "ragged")
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    ok, rep = within_tol(C, ref)
+    assert ok, rep
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 1, 11008), (11008, 16, 4096), (256, 128, 4096), (70, 7, 256),
+                                   (40, 33, 320), (64, 2, 128)])
+def test_literal_bit_exact(M, N, K):
+    g = rng("lit", M, N, K)
+    G = (K + 127) // 128
+    qA = g.integers(0, 16, (M, K))
+    A_q = quant.pack_rows(qA)
+    sA = g.uniform(0.001, 0.02, (M, G)).astype(np.float16)
+    sB = g.uniform(0.001, 0.02, (G, N)).astype(np.float16)
+    hb = N // 2
+    B_q = g.integers(0, 256, (K, hb)).astype(np.uint8) if hb > 0 else None
+    C = run_int4(A_q, sA, None, B_q, sB, None, M, N, K, mode=LIT)
+    rows = np.arange(M) if M <= 512 else np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 32)]))
+    Bo = B_q if B_q is not None else np.zeros((K, 1), np.uint8)
+    ref = oracle.gemm_int4_literal(A_q[rows], sA[rows], Bo, sB, len(rows), N, K)
+    assert np.array_equal(f16bits(C[rows]), f16bits(ref))
+    if N == 1:
+        assert np.all(f16bits(C) == 0)
+
+
+def test_quantizer_round_trip_through_kernel():
+    # quantise real-valued weights/activations, multiply, compare with the
+    # float64 product of the dequantised operands
+    g = rng("quant")
+    M, N, K = 256, 16, 1024
+    W = g.standard_normal((M, K)) * 0.02
+    X = g.standard_normal((K, N))
+    A_q, sA, zA = quant.quantize_rows(W)
+    B_q, sB, zB = quant.quantize_cols(X)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    ref = quant.dequantize_rows(A_q, sA, zA, K) @ quant.dequantize_rows(
+        quant.pack_rows(quant.unpack_cols(B_q, N).T), sB.T, zB.T, K).T
+    ok, rep = within_tol(C, ref)
+    assert ok, rep

@@ -1,0 +1,103 @@
+"""GPU parity of the INT8 entry points against the oracle: bit-exact.
+
+int32 accumulators are compared through clove_gemm_int8_acc32 (the same
+kernels with an integer epilogue) and the fp16 outputs are compared bit for
+bit: C = fp16(float(acc) * scale) has exactly one well-defined rounding chain.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import empty_f16, f16bits, rng, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _cg():
+    import clove_compute_amd as cg
+    return cg
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def run_acc32(A, B, za=0, zb=0):
+    import torch
+    M, K = A.shape
+    N = B.shape[1]
+    acc = torch.empty(M, N, dtype=torch.int32, device="cuda")
+    _cg().gemm_int8_acc32(to_dev(A), to_dev(B), acc, M, N, K, za, zb)
+    _sync()
+    return acc.cpu().numpy()
+
+
+@pytest.mark.parametrize("M", [1, 128])
+def test_config3_w8a8_rowcol(M):
+    # weights int8 U[-127,127] with per-channel fp16 scales, activations int8
+    # with per-token fp16 scales, zero points 0
+    N = K = 4096
+    g = rng("cfg3", M)
+    A = g.integers(-127, 128, (M, K)).astype(np.int8)
+    B = g.integers(-127, 128, (K, N)).astype(np.int8)
+    sa = g.uniform(0.001, 0.02, M).astype(np.float16)
+    sb = g.uniform(0.001, 0.02, N).astype(np.float16)
+    C = empty_f16(M, N)
+    _cg().gemm_int8_rowcol(to_dev(A), to_dev(B), to_dev(sa), to_dev(sb), C, M, N, K)
+    _sync()
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, min(M, 16))]))
+    Cref, accref = oracle.gemm_int8_rowcol(A[rows], B, sa[rows], sb)
+    assert np.array_equal(f16bits(to_host(C)[rows]), f16bits(Cref))
+    acc = run_acc32(A, B)
+    assert np.array_equal(acc[rows], accref)
+    # every accumulator at full size: float64 BLAS on integers is exact here
+    full = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(acc.astype(np.float64), full)
+
+
+@pytest.mark.parametrize("M,N,K,za,zb", [
+    (1, 4096, 4096, 0, 0), (1, 512, 1000, 3, -5), (3, 256, 256, -128, 127), (4, 96, 64, 7, 7),
+    (64, 64, 64, 0, 0), (200, 130, 300, 5, -9), (129, 4096, 512, -3, 2), (37, 19, 45, 1, 1),
+    (512, 512, 512, 0, 0),
+])
+def test_per_tensor_bit_exact(M, N, K, za, zb):
+    g = rng("pt", M, N, K, za, zb)
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    sa, sb = np.float32(g.uniform(0.001, 0.05)), np.float32(g.uniform(0.001, 0.05))
+    C = empty_f16(M, N)
+    _cg().gemm_int8(to_dev(A), to_dev(B), C, M, N, K, float(sa), za, float(sb), zb)
+    _sync()
+    Cref, accref = oracle.gemm_int8(A, B, sa, za, sb, zb)
+    assert np.array_equal(f16bits(to_host(C)), f16bits(Cref))
+    assert np.array_equal(run_acc32(A, B, za, zb), accref)
+
+
+def test_reference_race_region_is_correct():
+    # the reference kernel's 64x64 tiles let threads write outside their tile
+    # (src/kernels/gemm_int8.cu:29-34 vs :9-10); every element here must equal
+    # the per-element formula, including far from the first tile
+    g = rng("race")
+    M, N, K = 192, 320, 96
+    A = g.integers(-50, 50, (M, K)).astype(np.int8)
+    B = g.integers(-50, 50, (K, N)).astype(np.int8)
+    C = empty_f16(M, N)
+    _cg().gemm_int8(to_dev(A), to_dev(B), C, M, N, K, 0.01, 0, 0.02, 0)
+    _sync()
+    Cref, _ = oracle.gemm_int8(A, B, np.float32(0.01), 0, np.float32(0.02), 0)
+    assert np.array_equal(f16bits(to_host(C)), f16bits(Cref))
+
+
+def test_broadcast_rowcol_equals_per_tensor():
+    g = rng("bcast")
+    M, N, K = 64, 256, 512
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    s1, s2 = np.float16(0.0137), np.float16(0.0061)
+    C1, C2 = empty_f16(M, N), empty_f16(M, N)
+    _cg().gemm_int8(to_dev(A), to_dev(B), C1, M, N, K, float(s1), 2, float(s2), -3)
+    _cg().gemm_int8_rowcol(to_dev(A), to_dev(B), to_dev(np.full(M, s1)), to_dev(np.full(N, s2)), C2,
+                           M, N, K, 2, -3)
+    _sync()
+    assert np.array_equal(f16bits(to_host(C1)), f16bits(to_host(C2)))
