@@ -155,7 +155,7 @@ clove_status_t run_mfma(Params p, int batch, int num_cus, hipStream_t stream) {
     p.tiles_m = cdiv(p.M, T::BM);
     p.tiles_n = cdiv(p.N, T::BN);
     const int tiles = p.tiles_m * p.tiles_n * batch;
-    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, T::BK, 2 * num_cus, 4);
+    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, T::BK, num_cus, 2 * num_cus, 4);
     p.nsplit = sp.nsplit;
     p.k_per_split = sp.k_per_split;
     p.ws = nullptr;
@@ -170,8 +170,12 @@ clove_status_t run_mfma(Params p, int batch, int num_cus, hipStream_t stream) {
     }
     const int64_t grid = (int64_t)tiles * p.nsplit;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
-    hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>>), dim3((unsigned)grid),
-                       dim3(T::NT), 0, stream, p);
+    if (p.nsplit > 1)
+        hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, true>),
+                           dim3((unsigned)grid), dim3(T::NT), 0, stream, p);
+    else
+        hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, false>),
+                           dim3((unsigned)grid), dim3(T::NT), 0, stream, p);
     return check_launch();
 }
 

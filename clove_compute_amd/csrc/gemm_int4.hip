@@ -49,9 +49,11 @@ __global__ void fill_u16(uint16_t* p, size_t n, uint16_t v) {
         p[i] = v;
 }
 
-// LDS layout (dynamic): Bw [NV][4*nch] u32 | Bsum [NV][nch] int | Bs [NV][G] f32 | Bz [NV][G] int
-__host__ __device__ inline size_t gemv_lds_bytes(int nv, int nch, int G) {
-    return (size_t)nv * ((size_t)4 * nch * 4 + (size_t)nch * 4 + (size_t)G * 8);
+// LDS layout (dynamic): raw B bytes [K * ldb] (staging, rounded up to 16 bytes) |
+// Bw [NV][4*nch] u32 | Bsum [NV][nch] int | Bs [NV][G] f32 | Bz [NV][G] int
+__host__ __device__ inline size_t gemv_lds_bytes(int nv, int nch, int G, int K, int ldb) {
+    return (size_t)nv * ((size_t)4 * nch * 4 + (size_t)nch * 4 + (size_t)G * 8) +
+           (((size_t)K * ldb + 15) & ~(size_t)15);
 }
 
 template <int NV, int MODE, int LPR, bool ALIGNED>
@@ -62,7 +64,10 @@ __global__ void __launch_bounds__(256) int4_gemv(GemvParams p) {
     const int tid = threadIdx.x;
     const int nch = p.nch, K = p.K, G = p.G;
     const int KWP = 4 * nch;
-    unsigned* Bw = lds;
+    // raw bytes first so both the 16-byte staging stores and Bw stay aligned
+    uint8_t* Braw = reinterpret_cast<uint8_t*>(lds);
+    const int rawsz = p.cols_valid > 0 ? ((K * p.ldb + 15) & ~15) : 0;
+    unsigned* Bw = reinterpret_cast<unsigned*>(Braw + rawsz);
     int* Bsum = reinterpret_cast<int*>(Bw + NV * KWP);
     float* Bs = reinterpret_cast<float*>(Bsum + NV * nch);
     int* Bz = reinterpret_cast<int*>(Bs + NV * G);
@@ -106,7 +111,20 @@ __global__ void __launch_bounds__(256) int4_gemv(GemvParams p) {
     };
     load_batch(lr, a_cur, s_cur, z_cur);
 
-    // ---- stage B: nibble words in A's order, chunk sums, scales, zeros ----
+    // ---- stage B: raw bytes (16-byte loads), then nibble words in A's order ----
+    const int braw = p.cols_valid > 0 ? K * p.ldb : 0;
+    if ((reinterpret_cast<uintptr_t>(p.B) & 15) == 0) {
+        for (int i = tid; 16 * i < braw; i += 256) {
+            if (16 * i + 16 <= braw) {
+                *reinterpret_cast<u32x4*>(Braw + 16 * i) = *reinterpret_cast<const u32x4*>(p.B + 16 * i);
+            } else {
+                for (int j = 16 * i; j < braw; ++j) Braw[j] = p.B[j];
+            }
+        }
+    } else {
+        for (int i = tid; i < braw; i += 256) Braw[i] = p.B[i];
+    }
+    __syncthreads();
     for (int idx = tid; idx < NV * KWP; idx += 256) {
         const int n = idx / KWP, w = idx - n * KWP;
         unsigned word = 0;
@@ -115,7 +133,7 @@ __global__ void __launch_bounds__(256) int4_gemv(GemvParams p) {
             for (int j = 0; j < 8; ++j) {
                 const int k = 8 * w + j;
                 if (k < K) {
-                    const unsigned byte = p.B[(int64_t)k * p.ldb + (n >> 1)];
+                    const unsigned byte = Braw[k * p.ldb + (n >> 1)];
                     const unsigned nib = (n & 1) ? (byte & 0xfu) : (byte >> 4);
                     word |= nib << (8 * (j >> 1) + ((j & 1) ? 0 : 4));
                 }
@@ -231,8 +249,8 @@ constexpr size_t kMaxGemvLds = 150 * 1024;
 
 template <int NV, int MODE>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, hipStream_t stream) {
-    constexpr int LPR = 32;
-    const size_t lds = gemv_lds_bytes(NV, p.nch, p.G);
+    constexpr int LPR = 16;
+    const size_t lds = gemv_lds_bytes(NV, p.nch, p.G, p.K, p.ldb);
     const dim3 grid(cdiv(p.M, 256 / LPR));
     if (aligned) {
         auto k = int4_gemv<NV, MODE, LPR, true>;
@@ -272,7 +290,7 @@ clove_status_t run_mfma(mg::Params p, int cus, hipStream_t stream) {
     p.tiles_n = cdiv(p.N, T::BN);
     const int tiles = p.tiles_m * p.tiles_n;
     // splits on 128-wide group boundaries so every group is folded whole
-    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, 128, 2 * cus, 2);
+    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, 128, cus, 2 * cus, 2);
     p.nsplit = sp.nsplit;
     p.k_per_split = sp.k_per_split;
     if (p.nsplit > 1) {
@@ -317,7 +335,7 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
                            stream, a.C, n, (uint16_t)0);
         return check_launch();
     }
-    if (a.N <= 8 && gemv_lds_bytes(a.N <= 2 ? a.N : (a.N <= 4 ? 4 : 8), nch, G) <= kMaxGemvLds) {
+    if (a.N <= 8 && gemv_lds_bytes(a.N <= 2 ? a.N : (a.N <= 4 ? 4 : 8), nch, G, a.K, ldb) <= kMaxGemvLds) {
         GemvParams p{a.A, a.A_scale, a.A_zero, a.B, a.B_scale, a.B_zero, a.C,
                      a.M, a.N, a.K, G, ldb, cols_valid, nch};
         const bool aligned = aligned16(a.A) && (a.K % 32 == 0);

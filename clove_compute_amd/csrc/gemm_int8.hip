@@ -408,7 +408,7 @@ clove_status_t run_mfma(I8Params p, int cus, hipStream_t stream) {
     p.tiles_m = cdiv(p.M, BM);
     p.tiles_n = cdiv(p.N, BN);
     const int tiles = p.tiles_m * p.tiles_n;
-    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, BK, 2 * cus, 2);
+    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, BK, cus, 2 * cus, 2);
     p.nsplit = sp.nsplit;
     p.k_per_split = sp.k_per_split;
     const bool sums = (p.za != 0 || p.zb != 0) && p.K > 0;

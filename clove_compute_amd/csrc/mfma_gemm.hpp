@@ -496,7 +496,7 @@ struct Tile {
 
 enum Fold { kFoldNone = 0, kFoldB = 1, kFoldAB = 2 };
 
-template <class T, class LA, class LB, class EPI, int FOLD = kFoldNone>
+template <class T, class LA, class LB, class EPI, int FOLD = kFoldNone, bool SPLITK = true>
 __global__ void __launch_bounds__(T::NT) mfma_gemm(Params p) {
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, NT = T::NT, LDK = T::LDK;
     constexpr int WTM = BM / T::WGM;
@@ -612,7 +612,7 @@ __global__ void __launch_bounds__(T::NT) mfma_gemm(Params p) {
         __syncthreads();
     }
 
-    if (p.nsplit > 1) {
+    if (SPLITK && p.nsplit > 1) {
         const int tile_id = (tc.batch * p.tiles_m + tc.tm) * p.tiles_n + tc.tn;
         float* ws_tile = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
         float* mine = ws_tile + (int64_t)tc.split * (BM * BN);
@@ -668,11 +668,12 @@ struct SplitPlan {
     int k_per_split;
 };
 
-// Split K so that about `target` workgroups run, keeping >= min_ktiles K tiles
-// per split.
-inline SplitPlan plan_split(int tiles, int K, int bk, int target, int min_ktiles) {
+// Split K only when the tile grid leaves CUs idle (tiles < num_cus): then
+// about `target` workgroups run, each split keeping >= min_ktiles K tiles of
+// width bk.
+inline SplitPlan plan_split(int tiles, int K, int bk, int num_cus, int target, int min_ktiles) {
     SplitPlan sp{1, cdiv(K > 0 ? K : 1, bk) * bk};
-    if (K <= 0 || tiles >= target) return sp;
+    if (K <= 0 || tiles >= num_cus) return sp;
     const int ktiles = cdiv(K, bk);
     const int want = cdiv(target, tiles);
     const int maxs = max(1, ktiles / min_ktiles);

@@ -192,7 +192,7 @@ clove_status_t run_mfma(mg::Params p, int cus, hipStream_t stream) {
     p.tiles_n = cdiv(p.N, T::BN);
     const int tiles = p.tiles_m * p.tiles_n;
     // splits on 128-wide group boundaries so every group is folded whole
-    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, 128, 2 * cus, 2);
+    const mg::SplitPlan sp = mg::plan_split(tiles, p.K, 128, cus, 2 * cus, 2);
     p.nsplit = sp.nsplit;
     p.k_per_split = sp.k_per_split;
     if (p.nsplit > 1) {
