@@ -1,16 +1,20 @@
 // FP16 GEMM for gfx950: C = alpha * A @ B + beta * C, fp32 accumulation.
 //
 // Replaces the reference's gemm_fp16 (src/kernels/gemm_fp16.cu:277-305) and
-// gemm_fp16_batched (:366-383).  Two kernels:
+// gemm_fp16_batched (:366-383).  Kernels:
 //
+//  * dma::gemm_f16_dma (f16_dma_gemm.hpp) -- large aligned shapes: 256x256x64
+//    tiles, A staged by LDS DMA, B transposed through VGPRs, three-stage
+//    pipeline, one tile per CU.
 //  * mg::mfma_gemm with the fp16 row loader for A and the transposing fp16
 //    column loader for B (mfma_gemm.hpp): LDS-tiled v_mfma_f32_32x32x16_f16,
 //    tile shape chosen per (M, N), split-K when the tile grid is too small to
-//    fill the CUs.
+//    fill the CUs; every other shape.
 //  * gemv_f16 -- M <= 4 decode shapes: B streamed once from HBM with 16 B
 //    loads, fp32 FMAs on the VALU, split-K over workgroups.
 #include "common.hpp"
 #include "dispatch.hpp"
+#include "f16_dma_gemm.hpp"
 #include "mfma_gemm.hpp"
 
 namespace clove {
@@ -179,6 +183,27 @@ clove_status_t run_mfma(Params p, int batch, int num_cus, hipStream_t stream) {
     return check_launch();
 }
 
+using BigTile = dma::Cfg<256, 256, 64, 2, 2>;
+
+// The DMA kernel's preconditions: 16-byte aligned operands, K a multiple of
+// the K tile, N a multiple of 8, every per-batch operand addressable with
+// 32-bit byte offsets.
+bool dma_eligible(const void* A, const void* B, const void* C, int M, int N, int K) {
+    return aligned16(A) && aligned16(B) && aligned16(C) && K > 0 && K % BigTile::BK == 0 &&
+           N % 8 == 0 && N >= 8 && M >= 1 && (int64_t)M * K * 2 < (1ll << 31) &&
+           (int64_t)K * N * 2 < (1ll << 31) && (int64_t)M * N * 2 < (1ll << 31);
+}
+
+clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N,
+                       int K, float alpha, float beta, hipStream_t stream) {
+    dma::Args a{A, B, C, M, N, K, alpha, beta, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N,
+                cdiv(M, BigTile::BM), cdiv(N, BigTile::BN)};
+    const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * batch;
+    if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
+    hipLaunchKernelGGL((dma::gemm_f16_dma<BigTile>), dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
+    return check_launch();
+}
+
 template <int MM>
 clove_status_t run_gemv(GemvParams p, int batch, int num_cus, hipStream_t stream) {
     p.col_blocks = cdiv(p.N, GV_COLS);
@@ -231,6 +256,8 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
     p.strideA = sA; p.strideB = sB; p.strideC = sC;
     const int cus = dev.num_cus;
     const int64_t big_tiles = (int64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
+    if (big_tiles >= cus / 2 && dma_eligible(A, B, C, M, N, K))
+        return run_dma(A, B, C, batch, M, N, K, alpha, beta, stream);
     if (aligned) {
         if (big_tiles >= cus / 2) return run_mfma<Tile<256, 256, 64, 2, 2>, true>(p, batch, cus, stream);
         if (M <= 32) return run_mfma<Tile<32, 128, 64, 1, 4>, true>(p, batch, cus, stream);

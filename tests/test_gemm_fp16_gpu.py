@@ -161,3 +161,68 @@ def test_repeat_calls_deterministic_split_k():
         torch.cuda.synchronize()
         outs.append(f16bits(to_host(C)))
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+# ---- the 256x256x64 DMA-staged kernel (large, aligned shapes) ----
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 512), (3000, 3000, 320), (4096, 2056, 128)])
+def test_big_tile_ragged_edges(M, N, K):
+    # tile grids >= half the CUs with ragged M / N edges (clamped loads)
+    g = rng("big", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.05).astype(np.float16)
+    C = run_fp16(A, B)
+    rows = np.unique(np.concatenate([[0, 255, 256, M - 1], g.integers(0, M, 40)]))
+    check_rows(A, B, C, rows)
+    assert np.all(np.isfinite(C.astype(np.float32)))
+
+
+def test_big_tile_every_element_small_integers():
+    # every element bit-exact: small-integer inputs make any summation order exact
+    M, N, K = 2304, 3840, 192
+    g = rng("big_int")
+    A = g.integers(-3, 4, (M, K)).astype(np.float16)
+    B = g.integers(-3, 4, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(f16bits(C), f16bits(exact.astype(np.float16)))
+
+
+def test_big_tile_alpha_beta():
+    M = N = 3072
+    K = 256
+    g = rng("big_ab")
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.05).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=1.5, beta=-0.75)
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 24)]))
+    check_rows(A, B, C, rows, C0, 1.5, -0.75)
+
+
+def test_big_tile_batched():
+    import torch
+    batch, M, N, K = 2, 2048, 2048, 128
+    g = rng("big_batched")
+    A = g.standard_normal((batch, M, K)).astype(np.float16)
+    B = (g.standard_normal((batch, K, N)) * 0.05).astype(np.float16)
+    dC = empty_f16(batch, M, N, fill=float("nan"))
+    _cg().gemm_fp16_batched(to_dev(A), to_dev(B), dC, batch, M, N, K, 1.0, 0.0)
+    torch.cuda.synchronize()
+    C = to_host(dC)
+    for b in range(batch):
+        rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 16)]))
+        ref = oracle.gemm_fp16_f64(A[b][rows], B[b])
+        ok, rep = within_tol(C[b][rows], ref)
+        assert ok, (b, rep)
+
+
+def test_big_shape_k_not_multiple_of_tile():
+    # K % 64 != 0 takes the generic MFMA kernel
+    M, N, K = 4096, 4096, 1000
+    g = rng("big_k1000")
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.05).astype(np.float16)
+    C = run_fp16(A, B)
+    rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 16)]))
+    check_rows(A, B, C, rows)
