@@ -52,6 +52,19 @@ __device__ __forceinline__ unsigned pack2h(float lo, float hi) {
 }
 
 // ---------------------------------------------------------------------------
+// Workgroup barrier for an LDS hand-off only: waits for this wave's LDS
+// operations (lgkmcnt) but not for its global loads still in flight, which
+// __syncthreads() would (its workgroup fence waits on vmcnt(0)).  The empty
+// asm statements keep the compiler from moving LDS accesses across it.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
 // split-K publication without whole-cache maintenance.
 //
 // Partials are written with agent-scope relaxed atomic stores (global_store

@@ -5,13 +5,13 @@
 // in the high nibble; B_q [K, ceil(N/2)] packed along N, even n in the high
 // nibble; scales/zeros [M, G] and [G, N], G = ceil(K/128).
 //
-//  * int4_gemv (N <= 8, the decode shapes) -- one group of LPR lanes streams
-//    one weight row with 16-byte loads (32 nibbles per lane per step).  The
-//    per-group integer partials are exact:
+//  * int4_gemv (N <= 8, the decode shapes) -- one wave streams one weight
+//    row with 16-byte loads, the whole row in flight at once.  The per-group
+//    integer partials are exact:
 //       P = sum qA*qB - zB*sum qA - zA*sum qB + cnt*zA*zB
 //    with sum qA*qB from v_dot8_u32_u4 on nibble words, the B words (in A's
 //    nibble order) and their chunk sums staged once per workgroup in LDS.
-//    Group-wise: acc += (sA*sB) * float(P) per 32-k chunk, fp32.
+//    Group-wise: acc += (sA*sB) * float(P_g), fp32.
 //    Literal: int32 S accumulates sum (qA-8)(qB-8) over all K.
 //  * larger N -- the shared MFMA GEMM (mfma_gemm.hpp) with INT4 loaders that
 //    unpack both operands to the exact integers q - z in fp16 on their way to
@@ -49,193 +49,251 @@ __global__ void fill_u16(uint16_t* p, size_t n, uint16_t v) {
         p[i] = v;
 }
 
-// LDS layout (dynamic): raw B bytes [K * ldb] (staging, rounded up to 16 bytes) |
-// Bw [NV][4*nch] u32 | Bsum [NV][nch] int | Bs [NV][G] f32 | Bz [NV][G] int
-__host__ __device__ inline size_t gemv_lds_bytes(int nv, int nch, int G, int K, int ldb) {
-    return (size_t)nv * ((size_t)4 * nch * 4 + (size_t)nch * 4 + (size_t)G * 8) +
-           (((size_t)K * ldb + 15) & ~(size_t)15);
+// LDS layout (dynamic), per column n < NV:
+//   Bw [NV][4*nch] u32   B nibbles of 8 k in A's order (zero for k >= K)
+//   Bc [NV][nch]   int4  per 32-k chunk c with cnt valid k, sb = sum qB:
+//        group-wise {zB, sb - cnt zB, bits(sB), 0}   literal {64 cnt - 8 sb, 0, 0, 0}
+__host__ __device__ inline size_t gemv_lds_bytes(int nv, int nch, int /*G*/) {
+    return (size_t)nv * ((size_t)4 * nch * 4 + (size_t)nch * 16);
 }
 
-template <int NV, int MODE, int LPR, bool ALIGNED>
-__global__ void __launch_bounds__(256) int4_gemv(GemvParams p) {
+// B nibble word w (k = 8w .. 8w+7) of column n, in A's byte order: byte j holds
+// k = 8w + 2j in the high nibble and k = 8w + 2j + 1 in the low nibble
+__device__ __forceinline__ unsigned b_word(const GemvParams& p, int n, int w) {
+    const int k0 = 8 * w;
+    if (n >= p.cols_valid) return 0u;
+    if (p.ldb == 1 && k0 + 8 <= p.K && ((reinterpret_cast<uintptr_t>(p.B) + k0) & 7) == 0) {
+        // one byte per k row: B[k, 0] in the high nibble, B[k, 1] in the low one
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p.B + k0);
+        const unsigned ev = __builtin_amdgcn_perm(v.y, v.x, 0x06040200u);  // bytes k0, +2, +4, +6
+        const unsigned od = __builtin_amdgcn_perm(v.y, v.x, 0x07050301u);  // bytes k0+1, +3, +5, +7
+        if (n == 0) return (ev & 0xf0f0f0f0u) | ((od >> 4) & 0x0f0f0f0fu);
+        return ((ev << 4) & 0xf0f0f0f0u) | (od & 0x0f0f0f0fu);
+    }
+    unsigned word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int k = k0 + j;
+        if (k < p.K) {
+            const unsigned byte = p.B[(int64_t)k * p.ldb + (n >> 1)];
+            const unsigned nib = (n & 1) ? (byte & 0xfu) : (byte >> 4);
+            word |= nib << (8 * (j >> 1) + ((j & 1) ? 0 : 4));
+        }
+    }
+    return word;
+}
+
+// Each wave owns RPW consecutive rows of A.  Lane l takes the 16-byte chunks
+// c = l + 64u (32 k, a quarter of a 128-k group), u < UPR, of every row; all
+// of them (RPW * UPR <= 8 per lane) are loaded before the B staging, so the
+// whole weight stream is requested at once.  Per chunk and column the exact integer partial
+//     P = sum (qA - zA)(qB - zB) = sum qA qB - zB sum qA - zA (sb - cnt zB)
+// is formed with v_dot8_u32_u4 and added to the fp32 accumulator as
+// (sA sB) * P.  Literal mode sums (qA - 8)(qB - 8) as int32 over all K.
+// Zero points must lie in [-255, 255] (24-bit products).
+template <int NV, int MODE, int WPB, int RPW, int UPR, bool ALIGNED>
+__global__ void __launch_bounds__(WPB * 64) int4_gemv(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
-    constexpr int RPW = 256 / LPR;  // rows per workgroup
-    constexpr int UNR = 4;          // chunks in flight per lane
-    const int tid = threadIdx.x;
-    const int nch = p.nch, K = p.K, G = p.G;
-    const int KWP = 4 * nch;
-    // raw bytes first so both the 16-byte staging stores and Bw stay aligned
-    uint8_t* Braw = reinterpret_cast<uint8_t*>(lds);
-    const int rawsz = p.cols_valid > 0 ? ((K * p.ldb + 15) & ~15) : 0;
-    unsigned* Bw = reinterpret_cast<unsigned*>(Braw + rawsz);
-    int* Bsum = reinterpret_cast<int*>(Bw + NV * KWP);
-    float* Bs = reinterpret_cast<float*>(Bsum + NV * nch);
-    int* Bz = reinterpret_cast<int*>(Bs + NV * G);
+    constexpr int NT = WPB * 64;  // UPR: chunks per lane per row per batch
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = p.nch, K = p.K, G = p.G, KW = 4 * nch;
+    unsigned* Bw = lds;
+    i32x4* Bc = reinterpret_cast<i32x4*>(Bw + NV * KW);  // 16-byte aligned: KW % 4 == 0
 
-    const int row = blockIdx.x * RPW + tid / LPR;
-    const int lr = tid % LPR;
-    const bool row_ok = row < p.M;
-    const uint8_t* arow = p.A + (int64_t)row * (K / 2);
+    const int row0 = (blockIdx.x * WPB + wave) * RPW;
+    int ridx[RPW];  // rows past M read the last row and are not stored
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) ridx[r] = min(row0 + r, p.M - 1);
 
-    // ---- prefetch the first batch of A chunks (overlaps the B staging) ----
-    unsigned a_cur[UNR][4];
-    uint16_t s_cur[UNR], z_cur[UNR];
-    auto load_batch = [&](int c0, unsigned (&a)[UNR][4], uint16_t (&s)[UNR], uint16_t (&z)[UNR]) {
+    // ---- B for one byte per k row (N <= 2): raw bytes of this thread's 32-k
+    // chunks, loaded before the A stream so that waiting for them does not wait
+    // for A (loads complete in order) ----
+    constexpr int BCH = 2;  // B chunks per thread in the fast path
+    const bool bfast = p.ldb == 1 && NV <= 2 && nch <= BCH * NT &&
+                       (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 && (K & 31) == 0;
+    u32x4 braw[BCH][2];
+    if (bfast) {
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int c = c0 + u * LPR;
-            const bool in = row_ok && c < nch;
-            if constexpr (ALIGNED) {
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (in) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(arow + 16 * c));
-                a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
-            } else {
+        for (int i = 0; i < BCH; ++i) {
+            const int c = min(tid + i * NT, nch - 1);  // unconditional, see below
+            braw[i][0] = *reinterpret_cast<const u32x4*>(p.B + 32 * c);
+            braw[i][1] = *reinterpret_cast<const u32x4*>(p.B + 32 * c + 16);
+        }
+    }
+
+    // A chunks and their group scale / zero.  Loads are unconditional from
+    // clamped (valid) addresses and masked where used: a guarded load would
+    // become a branch whose merge makes the compiler wait for it right away.
+    u32x4 a[RPW][UPR];
+    uint16_t sah[RPW][UPR], zah[RPW][UPR];
+    auto load_batch = [&](int c0) {
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    unsigned w = 0;
+        for (int r = 0; r < RPW; ++r) {
+            const uint8_t* arow = p.A + (int64_t)ridx[r] * (K / 2);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int byte = 16 * c + 4 * d + e;
-                        const unsigned b = (in && 2 * byte < K) ? arow[byte] : 0u;
-                        w |= b << (8 * e);
+            for (int u = 0; u < UPR; ++u) {
+                const int cc = min(c0 + 64 * u + lane, nch - 1);
+                if constexpr (ALIGNED) {
+                    a[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(arow + 16 * cc));
+                } else {
+                    unsigned w[4];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        w[d] = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int byte = 16 * cc + 4 * d + e;
+                            const unsigned b = (2 * byte < K) ? arow[min(byte, K / 2 - 1)] : 0u;
+                            w[d] |= b << (8 * e);
+                        }
                     }
-                    a[u][d] = w;
+                    a[r][u] = u32x4{w[0], w[1], w[2], w[3]};
                 }
-            }
-            if constexpr (MODE == mg::kI4Groupwise) {
-                const int64_t gi = (int64_t)row * G + (c >> 2);
-                s[u] = in ? p.A_scale[gi] : (uint16_t)0;
-                z[u] = in ? p.A_zero[gi] : (uint16_t)0;
+                if constexpr (MODE == mg::kI4Groupwise) {
+                    const int64_t gi = (int64_t)ridx[r] * G + (cc >> 2);
+                    sah[r][u] = p.A_scale[gi];
+                    zah[r][u] = p.A_zero[gi];
+                }
             }
         }
     };
-    load_batch(lr, a_cur, s_cur, z_cur);
+    load_batch(0);
 
-    // ---- stage B: raw bytes (16-byte loads), then nibble words in A's order ----
-    const int braw = p.cols_valid > 0 ? K * p.ldb : 0;
-    if ((reinterpret_cast<uintptr_t>(p.B) & 15) == 0) {
-        for (int i = tid; 16 * i < braw; i += 256) {
-            if (16 * i + 16 <= braw) {
-                *reinterpret_cast<u32x4*>(Braw + 16 * i) = *reinterpret_cast<const u32x4*>(p.B + 16 * i);
-            } else {
-                for (int j = 16 * i; j < braw; ++j) Braw[j] = p.B[j];
-            }
-        }
-    } else {
-        for (int i = tid; i < braw; i += 256) Braw[i] = p.B[i];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < NV * KWP; idx += 256) {
-        const int n = idx / KWP, w = idx - n * KWP;
-        unsigned word = 0;
-        if (n < p.cols_valid) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int k = 8 * w + j;
-                if (k < K) {
-                    const unsigned byte = Braw[k * p.ldb + (n >> 1)];
-                    const unsigned nib = (n & 1) ? (byte & 0xfu) : (byte >> 4);
-                    word |= nib << (8 * (j >> 1) + ((j & 1) ? 0 : 4));
-                }
-            }
-        }
-        Bw[idx] = word;
-    }
-    if constexpr (MODE == mg::kI4Groupwise) {
-        for (int idx = tid; idx < NV * G; idx += 256) {
-            const int n = idx / G, g = idx - n * G;
-            const bool in = n < p.N;
-            Bs[idx] = in ? h2f(p.B_scale[(int64_t)g * p.N + n]) : 0.0f;
-            Bz[idx] = in ? (int)rintf(h2f(p.B_zero[(int64_t)g * p.N + n])) : 0;
-        }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < NV * nch; idx += 256) {
-        const int n = idx / nch, c = idx - n * nch;
-        const unsigned* bw = Bw + n * KWP + 4 * c;
-        unsigned s = 0;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) s = __builtin_amdgcn_udot8(bw[d], kOnes, s, false);
-        Bsum[idx] = (int)s;
-    }
-    __syncthreads();
-
-    // ---- stream the row ----
-    float accf[NV];
-    int acci[NV];
-#pragma unroll
-    for (int n = 0; n < NV; ++n) { accf[n] = 0.0f; acci[n] = 0; }
-
-    for (int c0 = lr; c0 < nch; c0 += UNR * LPR) {
-        unsigned a_nxt[UNR][4];
-        uint16_t s_nxt[UNR], z_nxt[UNR];
-        const bool more = c0 + UNR * LPR < nch;
-        if (more) load_batch(c0 + UNR * LPR, a_nxt, s_nxt, z_nxt);
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int c = c0 + u * LPR;
-            if (c >= nch) break;
+    // ---- stage B once per workgroup ----
+    // per-chunk constants of column n (see the LDS layout)
+    auto chunk_consts = [&](int n, int c, unsigned sb) -> i32x4 {
+        const int cnt = min(32, K - 32 * c);
+        if constexpr (MODE == mg::kI4Groupwise) {
             const int g = c >> 2;
-            const int cnt = min(32, K - 32 * c);
-            unsigned sa = 0;
+            const bool in = n < p.N;
+            const int zb = in ? (int)rintf(h2f(p.B_zero[(int64_t)g * p.N + n])) : 0;
+            const float sbf = in ? h2f(p.B_scale[(int64_t)g * p.N + n]) : 0.0f;
+            return i32x4{zb, (int)sb - cnt * zb, bitcast<int>(sbf), 0};
+        } else {
+            return i32x4{64 * cnt - 8 * (int)sb, 0, 0, 0};
+        }
+    };
+    if (bfast) {
+        // chunk c: 32 bytes (k = 32c .. 32c+31) -> 4 words per column and its constants
 #pragma unroll
-            for (int d = 0; d < 4; ++d) sa = __builtin_amdgcn_udot8(a_cur[u][d], kOnes, sa, false);
-            int za = 0;
-            float fa = 0.0f;
-            if constexpr (MODE == mg::kI4Groupwise) {
-                za = (int)rintf(h2f(z_cur[u]));
-                fa = h2f(s_cur[u]);
-            }
+        for (int i = 0; i < BCH; ++i) {
+            const int c = tid + i * NT;
+            if (c >= nch) continue;
+            const unsigned v[8] = {braw[i][0].x, braw[i][0].y, braw[i][0].z, braw[i][0].w,
+                                   braw[i][1].x, braw[i][1].y, braw[i][1].z, braw[i][1].w};
 #pragma unroll
             for (int n = 0; n < NV; ++n) {
-                const u32x4 bw = *reinterpret_cast<const u32x4*>(Bw + n * KWP + 4 * c);
-                unsigned dot = __builtin_amdgcn_udot8(a_cur[u][0], bw.x, 0u, false);
-                dot = __builtin_amdgcn_udot8(a_cur[u][1], bw.y, dot, false);
-                dot = __builtin_amdgcn_udot8(a_cur[u][2], bw.z, dot, false);
-                dot = __builtin_amdgcn_udot8(a_cur[u][3], bw.w, dot, false);
-                const int sb = Bsum[n * nch + c];
-                if constexpr (MODE == mg::kI4Groupwise) {
-                    const int zb = Bz[n * G + g];
-                    const int P = (int)dot - zb * (int)sa - za * sb + cnt * za * zb;
-                    accf[n] = fmaf(fa * Bs[n * G + g], (float)P, accf[n]);
-                } else {
-                    if (n < p.cols_valid) acci[n] += (int)dot - 8 * (int)sa - 8 * sb + 64 * cnt;
+                unsigned w[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const unsigned ev = __builtin_amdgcn_perm(v[2 * d + 1], v[2 * d], 0x06040200u);
+                    const unsigned od = __builtin_amdgcn_perm(v[2 * d + 1], v[2 * d], 0x07050301u);
+                    w[d] = n == 0 ? ((ev & 0xf0f0f0f0u) | ((od >> 4) & 0x0f0f0f0fu))
+                                  : (((ev << 4) & 0xf0f0f0f0u) | (od & 0x0f0f0f0fu));
+                    if (n >= p.cols_valid) w[d] = 0u;
                 }
+                *reinterpret_cast<u32x4*>(Bw + n * KW + 4 * c) = u32x4{w[0], w[1], w[2], w[3]};
+                unsigned sb = __builtin_amdgcn_udot8(w[0], kOnes, 0u, false);
+                sb = __builtin_amdgcn_udot8(w[1], kOnes, sb, false);
+                sb = __builtin_amdgcn_udot8(w[2], kOnes, sb, false);
+                sb = __builtin_amdgcn_udot8(w[3], kOnes, sb, false);
+                Bc[n * nch + c] = chunk_consts(n, c, sb);
             }
         }
-        if (more) {
+        lds_barrier();
+    } else {
+        for (int idx = tid; idx < NV * KW; idx += NT) Bw[idx] = b_word(p, idx / KW, idx % KW);
+        lds_barrier();
+        for (int idx = tid; idx < NV * nch; idx += NT) {
+            const int n = idx / nch, c = idx - n * nch;
+            const u32x4 bw = *reinterpret_cast<const u32x4*>(Bw + n * KW + 4 * c);
+            unsigned sb = __builtin_amdgcn_udot8(bw.x, kOnes, 0u, false);
+            sb = __builtin_amdgcn_udot8(bw.y, kOnes, sb, false);
+            sb = __builtin_amdgcn_udot8(bw.z, kOnes, sb, false);
+            sb = __builtin_amdgcn_udot8(bw.w, kOnes, sb, false);
+            Bc[idx] = chunk_consts(n, c, sb);
+        }
+        lds_barrier();
+    }
+
+    float accf[RPW][NV];
+    int acci[RPW][NV];
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) {
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) a_cur[u][d] = a_nxt[u][d];
-                s_cur[u] = s_nxt[u];
-                z_cur[u] = z_nxt[u];
+        for (int n = 0; n < NV; ++n) { accf[r][n] = 0.0f; acci[r][n] = 0; }
+
+    for (int c0 = 0; c0 < nch; c0 += 64 * UPR) {
+        if (c0 > 0) load_batch(c0);
+#pragma unroll
+        for (int u = 0; u < UPR; ++u) {
+            if (c0 + 64 * u >= nch) break;  // uniform across the wave
+            const int c = c0 + 64 * u + lane;
+            const int cs = min(c, nch - 1);  // lanes past the end compute garbage, masked below
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const bool valid = row0 + r < p.M && c < nch;
+                const u32x4 av = a[r][u];
+                unsigned sa = __builtin_amdgcn_udot8(av.x, kOnes, 0u, false);
+                sa = __builtin_amdgcn_udot8(av.y, kOnes, sa, false);
+                sa = __builtin_amdgcn_udot8(av.z, kOnes, sa, false);
+                sa = __builtin_amdgcn_udot8(av.w, kOnes, sa, false);
+                int za = 0;
+                float fa = 0.0f;
+                if constexpr (MODE == mg::kI4Groupwise) {
+                    za = (int)rintf(h2f(zah[r][u]));
+                    fa = valid ? h2f(sah[r][u]) : 0.0f;
+                }
+#pragma unroll
+                for (int n = 0; n < NV; ++n) {
+                    const u32x4 bw = *reinterpret_cast<const u32x4*>(Bw + n * KW + 4 * cs);
+                    const i32x4 bc = Bc[n * nch + cs];
+                    unsigned dot = __builtin_amdgcn_udot8(av.x, bw.x, 0u, false);
+                    dot = __builtin_amdgcn_udot8(av.y, bw.y, dot, false);
+                    dot = __builtin_amdgcn_udot8(av.z, bw.z, dot, false);
+                    dot = __builtin_amdgcn_udot8(av.w, bw.w, dot, false);
+                    if constexpr (MODE == mg::kI4Groupwise) {
+                        // |terms| < 2^24 for zero points in [-255, 255]: 24-bit products are exact
+                        const int P = (int)dot - __mul24(bc.x, (int)sa) - __mul24(za, bc.y);
+                        accf[r][n] = fmaf(fa * bitcast<float>(bc.z), (float)P, accf[r][n]);
+                    } else {
+                        const int P = (int)dot - 8 * (int)sa + bc.x;
+                        acci[r][n] += (valid && n < p.cols_valid) ? P : 0;
+                    }
+                }
             }
         }
     }
 
-    // ---- reduce over the LPR lanes of the row (fixed butterfly order) ----
+    // ---- reduce over the wave (fixed butterfly order) ----
 #pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) {
+    for (int off = 32; off > 0; off >>= 1) {
 #pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            if constexpr (MODE == mg::kI4Groupwise) accf[n] += __shfl_xor(accf[n], off);
-            else acci[n] += __shfl_xor(acci[n], off);
-        }
-    }
-    if (row_ok && lr == 0) {
+        for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int n = 0; n < NV; ++n) {
-            if (n >= p.N) break;
-            float r;
-            if constexpr (MODE == mg::kI4Groupwise) {
-                r = accf[n];
-            } else {
-                const float a_s = h2f(p.A_scale[(int64_t)row * G + (G - 1)]);
-                const float b_s = h2f(p.B_scale[(int64_t)(G - 1) * p.N + n]);
-                r = ((float)acci[n] * a_s) * b_s;
+            for (int n = 0; n < NV; ++n) {
+                if constexpr (MODE == mg::kI4Groupwise) accf[r][n] += __shfl_xor(accf[r][n], off);
+                else acci[r][n] += __shfl_xor(acci[r][n], off);
             }
-            p.C[(int64_t)row * p.N + n] = f2h(r);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int row = row0 + r;
+            if (row >= p.M) break;
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                if (n >= p.N) break;
+                float v;
+                if constexpr (MODE == mg::kI4Groupwise) {
+                    v = accf[r][n];
+                } else {
+                    const float a_s = h2f(p.A_scale[(int64_t)row * G + (G - 1)]);
+                    const float b_s = h2f(p.B_scale[(int64_t)(G - 1) * p.N + n]);
+                    v = ((float)acci[r][n] * a_s) * b_s;
+                }
+                p.C[(int64_t)row * p.N + n] = f2h(v);
+            }
         }
     }
 }
@@ -247,27 +305,30 @@ namespace {
 
 constexpr size_t kMaxGemvLds = 150 * 1024;
 
+template <int NV, int MODE, int RPW, int UPR>
+clove_status_t run_gemv_shape(const GemvParams& p, bool aligned, hipStream_t stream) {
+    constexpr int WPB = 16;  // waves per workgroup
+    const size_t lds = gemv_lds_bytes(NV, p.nch, p.G);
+    const dim3 grid(cdiv(p.M, WPB * RPW));
+    auto k = aligned ? int4_gemv<NV, MODE, WPB, RPW, UPR, true> : int4_gemv<NV, MODE, WPB, RPW, UPR, false>;
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+        return CLOVE_ERR_LAUNCH;
+    hipLaunchKernelGGL(k, grid, dim3(WPB * 64), lds, stream, p);
+    return check_launch();
+}
+
+// Up to 8 chunk loads per lane in flight: long rows take a wave each (rows of
+// more than 512 chunks in batches of 8 per lane), short rows share a wave.
 template <int NV, int MODE>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, hipStream_t stream) {
-    constexpr int LPR = 16;
-    const size_t lds = gemv_lds_bytes(NV, p.nch, p.G, p.K, p.ldb);
-    const dim3 grid(cdiv(p.M, 256 / LPR));
-    if (aligned) {
-        auto k = int4_gemv<NV, MODE, LPR, true>;
-        if (lds > 64 * 1024 &&
-            hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return CLOVE_ERR_LAUNCH;
-        hipLaunchKernelGGL(k, grid, dim3(256), lds, stream, p);
-    } else {
-        auto k = int4_gemv<NV, MODE, LPR, false>;
-        if (lds > 64 * 1024 &&
-            hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return CLOVE_ERR_LAUNCH;
-        hipLaunchKernelGGL(k, grid, dim3(256), lds, stream, p);
-    }
-    return check_launch();
+    const int cpl = cdiv(p.nch, 64);  // chunks per lane per row
+    if (cpl >= 7) return run_gemv_shape<NV, MODE, 1, 8>(p, aligned, stream);
+    if (cpl >= 5) return run_gemv_shape<NV, MODE, 1, 6>(p, aligned, stream);
+    if (cpl >= 3) return run_gemv_shape<NV, MODE, 2, 4>(p, aligned, stream);
+    if (cpl == 2) return run_gemv_shape<NV, MODE, 4, 2>(p, aligned, stream);
+    return run_gemv_shape<NV, MODE, 8, 1>(p, aligned, stream);
 }
 
 template <int MODE>
@@ -335,7 +396,7 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
                            stream, a.C, n, (uint16_t)0);
         return check_launch();
     }
-    if (a.N <= 8 && gemv_lds_bytes(a.N <= 2 ? a.N : (a.N <= 4 ? 4 : 8), nch, G, a.K, ldb) <= kMaxGemvLds) {
+    if (a.N <= 8 && gemv_lds_bytes(a.N <= 2 ? a.N : (a.N <= 4 ? 4 : 8), nch, G) <= kMaxGemvLds) {
         GemvParams p{a.A, a.A_scale, a.A_zero, a.B, a.B_scale, a.B_zero, a.C,
                      a.M, a.N, a.K, G, ldb, cols_valid, nch};
         const bool aligned = aligned16(a.A) && (a.K % 32 == 0);
