@@ -11,7 +11,8 @@
 //    tile shape chosen per (M, N), split-K when the tile grid is too small to
 //    fill the CUs; every other shape.
 //  * gemv_f16 -- M <= 4 decode shapes: B streamed once from HBM with 16 B
-//    loads, fp32 FMAs on the VALU, split-K over workgroups.
+//    loads (a 256 x 256 tile per workgroup, all in flight), fp32 FMAs on the
+//    VALU, split-K over workgroups.
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "f16_dma_gemm.hpp"
@@ -23,9 +24,14 @@ namespace fp16 {
 using namespace hw;
 
 // ---------------------------------------------------------------------------
-// GEMV path for M <= 4 (decode).  Workgroup = 256 threads = 32 column lanes x
-// 8 K lanes; each column lane owns 8 consecutive columns (one 16 B load per K
-// row), so one wave covers 2 K rows x 256 columns (2 x 512 B contiguous).
+// GEMV path for M <= 4 (decode).  A workgroup of 1024 threads owns 256
+// columns x 256 k-rows of B: thread (kl, cl) = (tid / 32, tid % 32) loads the
+// 16 bytes of columns 8cl..8cl+7 of rows kl + 32j, j < 8, so each wave
+// instruction reads two full 512-byte row segments and the whole 128 KB tile is
+// requested at once.  Loads are unconditional from clamped addresses (masked
+// at use).  Partials: wave halves, then the 16 waves through LDS (fixed
+// order), then the K splits, summed by the last workgroup to arrive (coherent
+// stores and loads, split order).
 // ---------------------------------------------------------------------------
 struct GemvParams {
     const uint16_t* A;
@@ -35,23 +41,22 @@ struct GemvParams {
     float alpha, beta;
     int64_t strideA, strideB, strideC;
     int col_blocks;   // cdiv(N, 256)
-    int nsplit;
-    int k_per_split;  // multiple of 8
+    int nsplit;       // cdiv(K, 256)
     float* ws;
     unsigned* counters;
 };
 
 constexpr int GV_COLS = 256;
-constexpr int GV_KL = 8;      // K lanes per workgroup
-constexpr int GV_UNROLL = 8;  // B rows in flight per thread
+constexpr int GV_KL = 32;                 // k lanes
+constexpr int GV_RPT = 8;                 // rows per thread
+constexpr int GV_ROWS = GV_KL * GV_RPT;   // k rows per workgroup
 
 template <int MM>
-__global__ void __launch_bounds__(256) gemv_f16(GemvParams p) {
-    __shared__ float red[GV_KL][MM][GV_COLS];
+__global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
+    __shared__ float red[16][MM][GV_COLS];
     __shared__ int s_last;
     const int tid = threadIdx.x;
-    const int cl = tid & 31;
-    const int kl = tid >> 5;
+    const int cl = tid & 31, kl = tid >> 5, wave = tid >> 6;
     int bid = blockIdx.x;
     const int split = bid % p.nsplit;
     bid /= p.nsplit;
@@ -63,74 +68,96 @@ __global__ void __launch_bounds__(256) gemv_f16(GemvParams p) {
     const int M = p.M, N = p.N, K = p.K;
     const int n = cb * GV_COLS + cl * 8;
     const bool col_ok = n < N;
-    const int kbeg = split * p.k_per_split;
-    const int kend = min(K, kbeg + p.k_per_split);
+    const int nc = min(n, N - 8);
+    const int kbeg = split * GV_ROWS;
+
+    u32x4 bv[GV_RPT];
+#pragma unroll
+    for (int j = 0; j < GV_RPT; ++j) {
+        const int k = min(kbeg + kl + GV_KL * j, K - 1);
+        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + (int64_t)k * N + nc));
+    }
+    uint16_t xa[MM][GV_RPT];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int j = 0; j < GV_RPT; ++j)
+            xa[m][j] = A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + GV_KL * j, K - 1)];
 
     float acc[MM][8];
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[m][e] = 0.0f;
-
-    for (int k = kbeg + kl; k < kend; k += GV_KL * GV_UNROLL) {
-        u32x4 bv[GV_UNROLL];
 #pragma unroll
-        for (int u = 0; u < GV_UNROLL; ++u) {
-            const int kk = k + u * GV_KL;
-            bv[u] = (col_ok && kk < kend)
-                        ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + (int64_t)kk * N + n))
-                        : u32x4{0u, 0u, 0u, 0u};
-        }
+    for (int j = 0; j < GV_RPT; ++j) {
+        const bool row_ok = kbeg + kl + GV_KL * j < K;
+        float bf[8];
+        bf[0] = h2f(bv[j].x & 0xffffu); bf[1] = h2f(bv[j].x >> 16);
+        bf[2] = h2f(bv[j].y & 0xffffu); bf[3] = h2f(bv[j].y >> 16);
+        bf[4] = h2f(bv[j].z & 0xffffu); bf[5] = h2f(bv[j].z >> 16);
+        bf[6] = h2f(bv[j].w & 0xffffu); bf[7] = h2f(bv[j].w >> 16);
 #pragma unroll
-        for (int u = 0; u < GV_UNROLL; ++u) {
-            const int kk = k + u * GV_KL;
-            if (kk >= kend) break;
-            float bf[8];
-            bf[0] = h2f(bv[u].x & 0xffffu); bf[1] = h2f(bv[u].x >> 16);
-            bf[2] = h2f(bv[u].y & 0xffffu); bf[3] = h2f(bv[u].y >> 16);
-            bf[4] = h2f(bv[u].z & 0xffffu); bf[5] = h2f(bv[u].z >> 16);
-            bf[6] = h2f(bv[u].w & 0xffffu); bf[7] = h2f(bv[u].w >> 16);
+        for (int m = 0; m < MM; ++m) {
+            const float a = (row_ok && m < M) ? h2f(xa[m][j]) : 0.0f;
 #pragma unroll
-            for (int m = 0; m < MM; ++m) {
-                const float a = (m < M) ? h2f(A[(int64_t)m * K + kk]) : 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(a, bf[e], acc[m][e]);
-            }
+            for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(a, bf[e], acc[m][e]);
         }
     }
-
-    // reduce the 8 K lanes (fixed order)
+    // the two k lanes of a wave (lanes l and l + 32), then the 16 waves
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red[kl][m][cl * 8 + e] = acc[m][e];
+        for (int e = 0; e < 8; ++e) acc[m][e] += __shfl_xor(acc[m][e], 32);
+    if ((tid & 32) == 0) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[wave][m][cl * 8 + e] = acc[m][e];
+    }
     __syncthreads();
-    // thread t now owns column t of the block for every row
-    const int col = tid;
+    // threads 0..255 own one column each from here on; every thread still
+    // takes part in the arrival barrier
+    const bool active = tid < GV_COLS;
+    const int col = active ? tid : 0;
     const int gn = cb * GV_COLS + col;
     float sum[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
         float s = 0.0f;
 #pragma unroll
-        for (int q = 0; q < GV_KL; ++q) s += red[q][m][col];
+        for (int w = 0; w < 16; ++w) s += red[w][m][col];
         sum[m] = s;
     }
 
     if (p.nsplit > 1) {
         const int tile_id = batch * p.col_blocks + cb;
         float* ws_tile = p.ws + (int64_t)tile_id * p.nsplit * (MM * GV_COLS);
+        if (active) {
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-            store_coherent(&ws_tile[(int64_t)split * MM * GV_COLS + m * GV_COLS + col], sum[m]);
+            for (int m = 0; m < MM; ++m)
+                store_coherent(&ws_tile[(int64_t)split * MM * GV_COLS + m * GV_COLS + col], sum[m]);
+        }
         if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
         for (int m = 0; m < MM; ++m) sum[m] = 0.0f;
-        for (int s = 0; s < p.nsplit; ++s)
+        // all partials in flight at once, then summed in split order
+        for (int s0 = 0; s0 < p.nsplit; s0 += 16) {
+            float part[16][MM];
 #pragma unroll
-            for (int m = 0; m < MM; ++m)
-                sum[m] += load_coherent(&ws_tile[(int64_t)s * MM * GV_COLS + m * GV_COLS + col]);
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+                    part[s][m] = s0 + s < p.nsplit
+                                     ? load_coherent(&ws_tile[(int64_t)(s0 + s) * MM * GV_COLS + m * GV_COLS + col])
+                                     : 0.0f;
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m) sum[m] += part[s][m];
+        }
     }
+    if (!active) return;
     if (gn < N) {
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
@@ -205,16 +232,10 @@ clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int ba
 }
 
 template <int MM>
-clove_status_t run_gemv(GemvParams p, int batch, int num_cus, hipStream_t stream) {
+clove_status_t run_gemv(GemvParams p, int batch, hipStream_t stream) {
     p.col_blocks = cdiv(p.N, GV_COLS);
+    p.nsplit = cdiv(p.K, GV_ROWS);
     const int tiles = p.col_blocks * batch;
-    // split K so that ~4 workgroups run per CU; each split keeps >= 64 rows
-    int want = cdiv(4 * num_cus, tiles);
-    int maxs = max(1, p.K / 64);
-    int ns = max(1, min(want, maxs));
-    int kps = cdiv(cdiv(p.K, ns), 8) * 8;
-    p.nsplit = cdiv(p.K, kps);
-    p.k_per_split = kps;
     p.ws = nullptr;
     p.counters = nullptr;
     if (p.nsplit > 1) {
@@ -225,7 +246,9 @@ clove_status_t run_gemv(GemvParams p, int batch, int num_cus, hipStream_t stream
         p.ws = s.partials;
         p.counters = s.counters;
     }
-    hipLaunchKernelGGL((gemv_f16<MM>), dim3(tiles * p.nsplit), dim3(256), 0, stream, p);
+    const int64_t grid = (int64_t)tiles * p.nsplit;
+    if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
+    hipLaunchKernelGGL((gemv_f16<MM>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
     return check_launch();
 }
 
@@ -244,10 +267,10 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
     const int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
 
     if (aligned && M <= 4 && K > 0) {
-        GemvParams g{A, B, C, M, N, K, alpha, beta, sA, sB, sC, 0, 1, 0, nullptr, nullptr};
-        if (M == 1) return run_gemv<1>(g, batch, dev.num_cus, stream);
-        if (M == 2) return run_gemv<2>(g, batch, dev.num_cus, stream);
-        return run_gemv<4>(g, batch, dev.num_cus, stream);
+        GemvParams g{A, B, C, M, N, K, alpha, beta, sA, sB, sC, 0, 1, nullptr, nullptr};
+        if (M == 1) return run_gemv<1>(g, batch, stream);
+        if (M == 2) return run_gemv<2>(g, batch, stream);
+        return run_gemv<4>(g, batch, stream);
     }
     Params p{};
     p.a = A; p.b = B; p.c = C;

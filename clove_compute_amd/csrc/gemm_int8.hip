@@ -13,8 +13,9 @@
 //    the row/column sums coming from a small pre-pass when a zero is non-zero.
 //    B [K,N] is N-contiguous: each thread transposes 4 K rows x 16 columns of
 //    bytes in registers (v_perm) on the way to LDS.
-//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads, int32 MADs on
-//    the VALU with the zero points subtracted directly, split-K over workgroups.
+//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads (a 256 x 256
+//    tile per workgroup, all in flight), int32 MADs on the VALU with the zero
+//    points subtracted directly, split-K over workgroups.
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "mfma_gemm.hpp"
@@ -288,85 +289,118 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
 // GEMV (M <= 4): 256 threads = 16 column lanes x 16 K lanes; a column lane
 // owns 16 consecutive columns (one 16-byte load per K row).
 // ---------------------------------------------------------------------------
+// A workgroup of 1024 threads owns 256 columns x 256 k-rows of B: thread
+// (kl, cl) = (tid / 16, tid % 16) loads the 16 bytes of columns 16cl..16cl+15
+// of rows kl + 64j, j < 4, so each wave instruction reads four full 256-byte
+// row segments and the whole 64 KB tile is requested at once.  Loads are
+// unconditional from clamped addresses (masked at use).  int32 partials:
+// within a wave (4 k lanes), across the 16 waves through LDS, then across the
+// K splits by the last workgroup to arrive (split order).
 constexpr int IV_COLS = 256;
-constexpr int IV_KL = 16;
-constexpr int IV_UNROLL = 8;
+constexpr int IV_KL = 64;
+constexpr int IV_RPT = 4;
+constexpr int IV_ROWS = IV_KL * IV_RPT;
 
 template <int MM, int OUT>
-__global__ void __launch_bounds__(256) int8_gemv(I8Params p, int col_blocks) {
-    __shared__ int red[IV_KL][MM][IV_COLS];
+__global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
+    __shared__ int red[16][MM][IV_COLS];
     __shared__ int s_last;
     const int tid = threadIdx.x;
-    const int cl = tid & 15, kl = tid >> 4;
+    const int cl = tid & 15, kl = tid >> 4, wave = tid >> 6;
     const int split = blockIdx.x % p.nsplit;
     const int cb = blockIdx.x / p.nsplit;
     const int M = p.M, N = p.N, K = p.K;
     const int n = cb * IV_COLS + cl * 16;
-    const bool col_ok = n < N;
-    const int kbeg = split * p.k_per_split;
-    const int kend = min(K, kbeg + p.k_per_split);
+    const int nc = min(n, N - 16);
+    const int kbeg = split * IV_ROWS;
+
+    u32x4 bv[IV_RPT];
+#pragma unroll
+    for (int j = 0; j < IV_RPT; ++j) {
+        const int k = min(kbeg + kl + IV_KL * j, K - 1);
+        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)k * N + nc));
+    }
+    int8_t xa[MM][IV_RPT];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int j = 0; j < IV_RPT; ++j)
+            xa[m][j] = p.A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + IV_KL * j, K - 1)];
 
     int acc[MM][16];
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[m][e] = 0;
-
-    for (int k = kbeg + kl; k < kend; k += IV_KL * IV_UNROLL) {
-        u32x4 bv[IV_UNROLL];
 #pragma unroll
-        for (int u = 0; u < IV_UNROLL; ++u) {
-            const int kk = k + u * IV_KL;
-            bv[u] = (col_ok && kk < kend)
-                        ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)kk * N + n))
-                        : u32x4{0u, 0u, 0u, 0u};
-        }
+    for (int j = 0; j < IV_RPT; ++j) {
+        const bool row_ok = kbeg + kl + IV_KL * j < K;
+        int bvals[16];
+        const unsigned w[4] = {bv[j].x, bv[j].y, bv[j].z, bv[j].w};
 #pragma unroll
-        for (int u = 0; u < IV_UNROLL; ++u) {
-            const int kk = k + u * IV_KL;
-            if (kk >= kend) break;
-            int bvals[16];
-            const unsigned w[4] = {bv[u].x, bv[u].y, bv[u].z, bv[u].w};
+        for (int e = 0; e < 16; ++e) bvals[e] = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                bvals[e] = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
+        for (int m = 0; m < MM; ++m) {
+            // |a - za|, |b - zb| <= 255: 24-bit products are exact
+            const int a = (row_ok && m < M) ? (int)xa[m][j] - p.za : 0;
 #pragma unroll
-            for (int m = 0; m < MM; ++m) {
-                const int a = (m < M) ? (int)p.A[(int64_t)m * K + kk] - p.za : 0;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[m][e] += a * bvals[e];
-            }
+            for (int e = 0; e < 16; ++e) acc[m][e] += __mul24(a, bvals[e]);
         }
     }
+    // the four k lanes of a wave (lanes l, l+16, l+32, l+48), then the 16 waves
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) red[kl][m][cl * 16 + e] = acc[m][e];
+        for (int e = 0; e < 16; ++e) {
+            acc[m][e] += __shfl_xor(acc[m][e], 16);
+            acc[m][e] += __shfl_xor(acc[m][e], 32);
+        }
+    if ((tid & 48) == 0) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) red[wave][m][cl * 16 + e] = acc[m][e];
+    }
     __syncthreads();
-    const int col = tid;
+    // threads 0..255 own one column each from here on; every thread still
+    // takes part in the arrival barrier
+    const bool active = tid < IV_COLS;
+    const int col = active ? tid : 0;
     const int gn = cb * IV_COLS + col;
     int sum[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
         int s = 0;
 #pragma unroll
-        for (int q = 0; q < IV_KL; ++q) s += red[q][m][col];
+        for (int q = 0; q < 16; ++q) s += red[q][m][col];
         sum[m] = s;
     }
     if (p.nsplit > 1) {
         float* ws_tile = p.ws + (int64_t)cb * p.nsplit * (MM * IV_COLS);
+        if (active) {
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-            store_coherent(&ws_tile[(int64_t)split * MM * IV_COLS + m * IV_COLS + col], __int_as_float(sum[m]));
+            for (int m = 0; m < MM; ++m)
+                store_coherent(&ws_tile[(int64_t)split * MM * IV_COLS + m * IV_COLS + col], __int_as_float(sum[m]));
+        }
         if (!splitk_arrive_is_last(&p.counters[cb], (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
         for (int m = 0; m < MM; ++m) sum[m] = 0;
-        for (int s = 0; s < p.nsplit; ++s)
+        for (int s0 = 0; s0 < p.nsplit; s0 += 16) {
+            int part[16][MM];
 #pragma unroll
-            for (int m = 0; m < MM; ++m)
-                sum[m] += __float_as_int(load_coherent(&ws_tile[(int64_t)s * MM * IV_COLS + m * IV_COLS + col]));
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+                    part[s][m] = s0 + s < p.nsplit ? __float_as_int(load_coherent(
+                                                         &ws_tile[(int64_t)(s0 + s) * MM * IV_COLS + m * IV_COLS + col]))
+                                                   : 0;
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m) sum[m] += part[s][m];
+        }
     }
-    if (gn < N) {
+    if (active && gn < N) {
 #pragma unroll
         for (int m = 0; m < MM; ++m)
             if (m < M) int8_store<OUT>(p, m, gn, sum[m]);
@@ -379,14 +413,10 @@ __global__ void __launch_bounds__(256) int8_gemv(I8Params p, int col_blocks) {
 namespace {
 
 template <int OUT>
-clove_status_t run_gemv(I8Params p, int cus, hipStream_t stream) {
+clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     const int col_blocks = cdiv(p.N, IV_COLS);
-    const int want = cdiv(4 * cus, col_blocks);
-    const int maxs = max(1, p.K / 64);
-    const int ns = max(1, min(want, maxs));
-    const int kps = cdiv(cdiv(p.K, ns), 16) * 16;
-    p.nsplit = cdiv(p.K, kps);
-    p.k_per_split = kps;
+    p.nsplit = cdiv(p.K, IV_ROWS);
+    p.k_per_split = IV_ROWS;
     if (p.nsplit > 1) {
         Scratch s;
         const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
@@ -396,10 +426,12 @@ clove_status_t run_gemv(I8Params p, int cus, hipStream_t stream) {
         p.ws = s.partials;
         p.counters = s.counters;
     }
-    const dim3 grid(col_blocks * p.nsplit);
-    if (p.M == 1) hipLaunchKernelGGL((int8_gemv<1, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
-    else if (p.M == 2) hipLaunchKernelGGL((int8_gemv<2, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
-    else hipLaunchKernelGGL((int8_gemv<4, OUT>), grid, dim3(256), 0, stream, p, col_blocks);
+    const int64_t g = (int64_t)col_blocks * p.nsplit;
+    if (g > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
+    const dim3 grid((unsigned)g);
+    if (p.M == 1) hipLaunchKernelGGL((int8_gemv<1, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
+    else if (p.M == 2) hipLaunchKernelGGL((int8_gemv<2, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
+    else hipLaunchKernelGGL((int8_gemv<4, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
     return check_launch();
 }
 
@@ -437,7 +469,7 @@ clove_status_t run_mfma(I8Params p, int cus, hipStream_t stream) {
 
 template <int OUT>
 clove_status_t dispatch(I8Params p, bool aligned, int cus, hipStream_t stream) {
-    if (aligned && p.M <= 4 && p.K > 0) return run_gemv<OUT>(p, cus, stream);
+    if (aligned && p.M <= 4 && p.K > 0 && p.N >= 16) return run_gemv<OUT>(p, stream);
     if (!aligned) return run_mfma<64, 64, 64, 2, 2, OUT, false>(p, cus, stream);
     if (p.M <= 64) return run_mfma<64, 128, 128, 2, 2, OUT, true>(p, cus, stream);
     if ((int64_t)cdiv(p.M, 256) * cdiv(p.N, 256) >= cus / 2)
