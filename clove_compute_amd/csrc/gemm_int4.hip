@@ -91,10 +91,10 @@ __device__ __forceinline__ unsigned b_word(const GemvParams& p, int n, int w) {
 // is formed with v_dot8_u32_u4 and added to the fp32 accumulator as
 // (sA sB) * P.  Literal mode sums (qA - 8)(qB - 8) as int32 over all K.
 // Zero points must lie in [-255, 255] (24-bit products).
-template <int NV, int MODE, int WPB, int RPW, int UPR, bool ALIGNED>
-__global__ void __launch_bounds__(WPB * 64) int4_gemv(GemvParams p) {
+template <int NV, int MODE, int RPW, int UPR, bool ALIGNED>
+__global__ void __launch_bounds__(1024) int4_gemv(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
-    constexpr int NT = WPB * 64;  // UPR: chunks per lane per row per batch
+    const int NT = blockDim.x, WPB = NT >> 6;  // UPR: chunks per lane per row per batch
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch = p.nch, K = p.K, G = p.G, KW = 4 * nch;
     unsigned* Bw = lds;
@@ -305,38 +305,59 @@ namespace {
 
 constexpr size_t kMaxGemvLds = 150 * 1024;
 
+// Rows per wave RPW and waves per workgroup: as many chunk loads per lane in
+// flight as fit (8), then enough workgroups to cover every CU.
+struct GemvShape {
+    int rpw, upr, wpb;
+};
+inline GemvShape gemv_shape(int rows, int nch, int cus) {
+    const int cpl = cdiv(nch, 64);
+    GemvShape g{1, 8, 16};
+    if (cpl >= 7) g = {1, 8, 16};
+    else if (cpl >= 5) g = {1, 6, 16};
+    else if (cpl >= 3) g = {2, 4, 16};
+    else if (cpl == 2) g = {4, 2, 16};
+    else g = {8, 1, 16};
+    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
+    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < cus) { g.rpw >>= 1; g.upr <<= 1; }
+    if (g.upr > 8) g.upr = 8;
+    return g;
+}
+
 template <int NV, int MODE, int RPW, int UPR>
-clove_status_t run_gemv_shape(const GemvParams& p, bool aligned, hipStream_t stream) {
-    constexpr int WPB = 16;  // waves per workgroup
+clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(NV, p.nch, p.G);
-    const dim3 grid(cdiv(p.M, WPB * RPW));
-    auto k = aligned ? int4_gemv<NV, MODE, WPB, RPW, UPR, true> : int4_gemv<NV, MODE, WPB, RPW, UPR, false>;
+    const dim3 grid(cdiv(p.M, wpb * RPW));
+    auto k = aligned ? int4_gemv<NV, MODE, RPW, UPR, true> : int4_gemv<NV, MODE, RPW, UPR, false>;
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, grid, dim3(WPB * 64), lds, stream, p);
+    hipLaunchKernelGGL(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
 }
 
-// Up to 8 chunk loads per lane in flight: long rows take a wave each (rows of
-// more than 512 chunks in batches of 8 per lane), short rows share a wave.
 template <int NV, int MODE>
-clove_status_t run_gemv(const GemvParams& p, bool aligned, hipStream_t stream) {
-    const int cpl = cdiv(p.nch, 64);  // chunks per lane per row
-    if (cpl >= 7) return run_gemv_shape<NV, MODE, 1, 8>(p, aligned, stream);
-    if (cpl >= 5) return run_gemv_shape<NV, MODE, 1, 6>(p, aligned, stream);
-    if (cpl >= 3) return run_gemv_shape<NV, MODE, 2, 4>(p, aligned, stream);
-    if (cpl == 2) return run_gemv_shape<NV, MODE, 4, 2>(p, aligned, stream);
-    return run_gemv_shape<NV, MODE, 8, 1>(p, aligned, stream);
+clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    const GemvShape g = gemv_shape(p.M, p.nch, cus);
+    // (rpw, upr) pairs keep rpw * upr <= 8 chunk loads per lane
+    if (g.rpw == 1) {
+        if (g.upr >= 8) return run_gemv_shape<NV, MODE, 1, 8>(p, g.wpb, aligned, stream);
+        if (g.upr >= 6) return run_gemv_shape<NV, MODE, 1, 6>(p, g.wpb, aligned, stream);
+        if (g.upr >= 4) return run_gemv_shape<NV, MODE, 1, 4>(p, g.wpb, aligned, stream);
+        return run_gemv_shape<NV, MODE, 1, 2>(p, g.wpb, aligned, stream);
+    }
+    if (g.rpw == 2) return run_gemv_shape<NV, MODE, 2, 4>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return run_gemv_shape<NV, MODE, 4, 2>(p, g.wpb, aligned, stream);
+    return run_gemv_shape<NV, MODE, 8, 1>(p, g.wpb, aligned, stream);
 }
 
 template <int MODE>
-clove_status_t gemv_by_n(const GemvParams& p, bool aligned, hipStream_t stream) {
-    if (p.N == 1) return run_gemv<1, MODE>(p, aligned, stream);
-    if (p.N == 2) return run_gemv<2, MODE>(p, aligned, stream);
-    if (p.N <= 4) return run_gemv<4, MODE>(p, aligned, stream);
-    return run_gemv<8, MODE>(p, aligned, stream);
+clove_status_t gemv_by_n(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    if (p.N == 1) return run_gemv<1, MODE>(p, aligned, cus, stream);
+    if (p.N == 2) return run_gemv<2, MODE>(p, aligned, cus, stream);
+    if (p.N <= 4) return run_gemv<4, MODE>(p, aligned, cus, stream);
+    return run_gemv<8, MODE>(p, aligned, cus, stream);
 }
 
 using mg::Tile;
@@ -400,8 +421,8 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
         GemvParams p{a.A, a.A_scale, a.A_zero, a.B, a.B_scale, a.B_zero, a.C,
                      a.M, a.N, a.K, G, ldb, cols_valid, nch};
         const bool aligned = aligned16(a.A) && (a.K % 32 == 0);
-        return literal ? gemv_by_n<mg::kI4Literal>(p, aligned, stream)
-                       : gemv_by_n<mg::kI4Groupwise>(p, aligned, stream);
+        return literal ? gemv_by_n<mg::kI4Literal>(p, aligned, dev.num_cus, stream)
+                       : gemv_by_n<mg::kI4Groupwise>(p, aligned, dev.num_cus, stream);
     }
     mg::Params p{};
     p.a = a.A; p.a_scale = a.A_scale; p.a_zero = a.A_zero;

@@ -6,12 +6,10 @@
 // (src/runtime/inference.cu:139-194, beta = 1 residual at :165-168, :191-194)
 // on INT4 weights.
 //
-//  * w4a16_gemv (T <= 4, decode) -- LPR lanes stream one weight row with
-//    16-byte loads.  Per 32-k chunk and token:
-//        sum_k x_k (q_k - z) = sum_k x_k (1024 + q_k) - (1024 + z) * sum_k x_k
-//    where 1024 + q is the fp16 bit pattern 0x6400 | q, the first sum is
-//    v_dot2_f32_f16 on (x pair, magic pair) and the chunk sums of x are staged
-//    in LDS with X once per workgroup.  acc += scale * that, in fp32.
+//  * w4a16_gemv (T <= 4, decode) -- a wave streams one or more weight rows
+//    with 16-byte loads, all in flight at once; the nibbles are turned into the
+//    exact fp16 integers q - z and dotted with X (staged in LDS) by
+//    v_dot2_f32_f16 in fp32; acc += scale * that per 32-k chunk.
 //  * larger T -- the shared MFMA GEMM (mfma_gemm.hpp): X rows as operand A,
 //    W rows unpacked to the exact integers q - z as operand B; the per-group
 //    fp32 partials are scaled by s[o,g] after each 128-wide group.
@@ -35,132 +33,171 @@ struct GemvParams {
     float alpha, beta;
 };
 
-// LDS (dynamic): Xs [TV][32*nch] fp16 | Xsum [TV][nch] f32
-__host__ __device__ inline size_t gemv_lds_bytes(int tv, int nch) {
-    return (size_t)tv * ((size_t)32 * nch * 2 + (size_t)nch * 4);
-}
+// LDS (dynamic): Xs [TV][32*nch] fp16, zero past K, each 8-k block stored in
+// the order x0 x2 x4 x6 x1 x3 x5 x7 (the order the weight pairs come out of
+// the nibble unpack below)
+__host__ __device__ inline size_t gemv_lds_bytes(int tv, int nch) { return (size_t)tv * 32 * nch * 2; }
 
-template <int TV, int LPR, bool ALIGNED>
-__global__ void __launch_bounds__(256) w4a16_gemv(GemvParams p) {
+// X position of k inside its 8-k block: even k first, then odd k
+__host__ __device__ constexpr int xperm(int k) { return (k & ~7) | ((k & 1) << 2) | ((k & 7) >> 1); }
+
+// Each wave owns RPW consecutive weight rows; lane l takes the 16-byte chunks
+// c = l + 64u (32 k), u < UPR, of every row, all loaded up front (X is staged
+// first so that waiting for it does not wait for the weights).  A weight dword
+// holds k = 8d..8d+7 with the even k in the high nibbles: the nibbles become
+// the fp16 values 1024 + q (v_perm against 0x64 bytes), minus 1024 + z gives
+// q - z exactly, and v_dot2_f32_f16 with the X pairs accumulates
+// sum_k x_k (q_k - z) in fp32 with exact products; acc += s * that per chunk.
+template <int TV, int RPW, int UPR, bool ALIGNED>
+__global__ void __launch_bounds__(1024) w4a16_gemv(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
-    constexpr int RPW = 256 / LPR;
-    constexpr int UNR = 4;
-    const int tid = threadIdx.x;
-    const int nch = p.nch, K = p.K, G = p.G;
-    const int KP = 32 * nch;
+    const int NT = blockDim.x, WPB = NT >> 6;  // waves per workgroup (rows / RPW)
+    constexpr int XPT = 4;  // X prefetch: 16-byte pieces per thread
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = p.nch, K = p.K, G = p.G, KP = 32 * nch;
     uint16_t* Xs = reinterpret_cast<uint16_t*>(lds);
-    float* Xsum = reinterpret_cast<float*>(Xs + TV * KP);
 
-    const int row = blockIdx.x * RPW + tid / LPR;
-    const int lr = tid % LPR;
-    const bool row_ok = row < p.O;
-    const uint8_t* wrow = p.W + (int64_t)row * (K / 2);
+    const int row0 = (blockIdx.x * WPB + wave) * RPW;
+    int ridx[RPW];  // rows past O read the last row and are not stored
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) ridx[r] = min(row0 + r, p.O - 1);
 
-    unsigned a_cur[UNR][4];
-    uint16_t s_cur[UNR], z_cur[UNR];
-    auto load_batch = [&](int c0, unsigned (&a)[UNR][4], uint16_t (&s)[UNR], uint16_t (&z)[UNR]) {
+    // ---- X: 16-byte pieces (8 k) into registers first ----
+    const int npieces = TV * KP / 8;
+    const bool xfast = npieces <= XPT * NT && (K & 7) == 0 && (reinterpret_cast<uintptr_t>(p.X) & 15) == 0;
+    u32x4 xr[XPT];
+    if (xfast) {
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int c = c0 + u * LPR;
-            const bool in = row_ok && c < nch;
-            if constexpr (ALIGNED) {
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (in) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 16 * c));
-                a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
-            } else {
+        for (int i = 0; i < XPT; ++i) {
+            const int q = min(tid + i * NT, npieces - 1);
+            const int t = q / (KP / 8), k8 = (q - t * (KP / 8)) * 8;
+            const int tt = min(t, p.T - 1), kk = min(k8, K - 8);
+            xr[i] = *reinterpret_cast<const u32x4*>(p.X + (int64_t)tt * K + kk);
+        }
+    }
+
+    // ---- the weight chunks and their group scale / zero (unconditional
+    // clamped loads, masked where used) ----
+    u32x4 a[RPW][UPR];
+    uint16_t sh[RPW][UPR], zh[RPW][UPR];
+    auto load_batch = [&](int c0) {
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    unsigned w = 0;
+        for (int r = 0; r < RPW; ++r) {
+            const uint8_t* wrow = p.W + (int64_t)ridx[r] * (K / 2);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int byte = 16 * c + 4 * d + e;
-                        const unsigned b = (in && 2 * byte < K) ? wrow[byte] : 0u;
-                        w |= b << (8 * e);
+            for (int u = 0; u < UPR; ++u) {
+                const int cc = min(c0 + 64 * u + lane, nch - 1);
+                if constexpr (ALIGNED) {
+                    a[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + 16 * cc));
+                } else {
+                    unsigned w[4];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        w[d] = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int byte = 16 * cc + 4 * d + e;
+                            const unsigned b = (2 * byte < K) ? wrow[min(byte, K / 2 - 1)] : 0u;
+                            w[d] |= b << (8 * e);
+                        }
                     }
-                    a[u][d] = w;
+                    a[r][u] = u32x4{w[0], w[1], w[2], w[3]};
                 }
+                const int64_t gi = (int64_t)ridx[r] * G + (cc >> 2);
+                sh[r][u] = p.scale[gi];
+                zh[r][u] = p.zero[gi];
             }
-            const int64_t gi = (int64_t)row * G + (c >> 2);
-            s[u] = in ? p.scale[gi] : (uint16_t)0;
-            z[u] = in ? p.zero[gi] : (uint16_t)0;
         }
     };
-    load_batch(lr, a_cur, s_cur, z_cur);
+    load_batch(0);
 
-    // ---- stage X (zero-padded to whole chunks) and its chunk sums ----
-    for (int idx = tid; idx < TV * KP; idx += 256) {
-        const int t = idx / KP, k = idx - t * KP;
-        Xs[idx] = (t < p.T && k < K) ? p.X[(int64_t)t * K + k] : (uint16_t)0;
+    // ---- stage X in the permuted order ----
+    if (xfast) {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+            const int q = tid + i * NT;
+            if (q >= npieces) continue;
+            const int t = q / (KP / 8), k8 = (q - t * (KP / 8)) * 8;
+            u32x4 v = xr[i];
+            if (t >= p.T || k8 >= K) v = u32x4{0u, 0u, 0u, 0u};
+            // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x2)(x4 x6)(x1 x3)(x5 x7)
+            const u32x4 o = {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                             __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+            *reinterpret_cast<u32x4*>(Xs + t * KP + k8) = o;
+        }
+    } else {
+        for (int idx = tid; idx < TV * KP; idx += NT) {
+            const int t = idx / KP, k = idx - t * KP;
+            Xs[t * KP + xperm(k)] = (t < p.T && k < K) ? p.X[(int64_t)t * K + k] : (uint16_t)0;
+        }
     }
-    __syncthreads();
-    for (int idx = tid; idx < TV * nch; idx += 256) {
-        const int t = idx / nch, c = idx - t * nch;
-        const uint16_t* xc = Xs + t * KP + 32 * c;
-        float s = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) s += h2f(xc[e]);
-        Xsum[idx] = s;
-    }
-    __syncthreads();
+    lds_barrier();
 
-    float acc[TV];
+    float acc[RPW][TV];
 #pragma unroll
-    for (int t = 0; t < TV; ++t) acc[t] = 0.0f;
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int t = 0; t < TV; ++t) acc[r][t] = 0.0f;
+    constexpr unsigned C64 = 0x64646464u;
 
-    for (int c0 = lr; c0 < nch; c0 += UNR * LPR) {
-        unsigned a_nxt[UNR][4];
-        uint16_t s_nxt[UNR], z_nxt[UNR];
-        const bool more = c0 + UNR * LPR < nch;
-        if (more) load_batch(c0 + UNR * LPR, a_nxt, s_nxt, z_nxt);
+    for (int c0 = 0; c0 < nch; c0 += 64 * UPR) {
+        if (c0 > 0) load_batch(c0);
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int c = c0 + u * LPR;
-            if (c >= nch) break;
-            unsigned mg16[16];
+        for (int u = 0; u < UPR; ++u) {
+            if (c0 + 64 * u >= nch) break;  // uniform across the wave
+            const int c = c0 + 64 * u + lane;
+            const int cs = min(c, nch - 1);  // lanes past the end: garbage, masked by s = 0
 #pragma unroll
-            for (int d = 0; d < 4; ++d) mg::nibbles_to_magic(a_cur[u][d], &mg16[4 * d]);
-            const float s = h2f(s_cur[u]);
-            const float zoff = 1024.0f + rintf(h2f(z_cur[u]));
+            for (int r = 0; r < RPW; ++r) {
+                const bool valid = row0 + r < p.O && c < nch;
+                const float sc = valid ? h2f(sh[r][u]) : 0.0f;
+                const f16x2 zz = mg::magic_zero(zh[r][u]);
+                f16x2 qz[16];
 #pragma unroll
-            for (int t = 0; t < TV; ++t) {
-                const u32x4* xv = reinterpret_cast<const u32x4*>(Xs + t * KP + 32 * c);
-                float dot = 0.0f;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const u32x4 x = xv[v];
-                    dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.x), bitcast<f16x2>(mg16[4 * v + 0]), dot, false);
-                    dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.y), bitcast<f16x2>(mg16[4 * v + 1]), dot, false);
-                    dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.z), bitcast<f16x2>(mg16[4 * v + 2]), dot, false);
-                    dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.w), bitcast<f16x2>(mg16[4 * v + 3]), dot, false);
+                for (int d = 0; d < 4; ++d) {
+                    const unsigned w = a[r][u][d];
+                    const unsigned hi = (w >> 4) & 0x0f0f0f0fu, lo = w & 0x0f0f0f0fu;
+                    qz[4 * d + 0] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04010400u)) - zz;
+                    qz[4 * d + 1] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04030402u)) - zz;
+                    qz[4 * d + 2] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04010400u)) - zz;
+                    qz[4 * d + 3] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04030402u)) - zz;
                 }
-                const float P = fmaf(-zoff, Xsum[t * nch + c], dot);
-                acc[t] = fmaf(s, P, acc[t]);
-            }
-        }
-        if (more) {
 #pragma unroll
-            for (int u = 0; u < UNR; ++u) {
+                for (int t = 0; t < TV; ++t) {
+                    const u32x4* xv = reinterpret_cast<const u32x4*>(Xs + t * KP + 32 * cs);
+                    float dot = 0.0f;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) a_cur[u][d] = a_nxt[u][d];
-                s_cur[u] = s_nxt[u];
-                z_cur[u] = z_nxt[u];
+                    for (int d = 0; d < 4; ++d) {
+                        const u32x4 x = xv[d];
+                        dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.x), qz[4 * d + 0], dot, false);
+                        dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.y), qz[4 * d + 1], dot, false);
+                        dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.z), qz[4 * d + 2], dot, false);
+                        dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.w), qz[4 * d + 3], dot, false);
+                    }
+                    acc[r][t] = fmaf(sc, dot, acc[r][t]);
+                }
             }
         }
     }
 #pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1)
+    for (int off = 32; off > 0; off >>= 1)
 #pragma unroll
-        for (int t = 0; t < TV; ++t) acc[t] += __shfl_xor(acc[t], off);
-    if (row_ok && lr < TV && lr < p.T) {
-        // lane t writes token t's output
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int t = 0; t < TV; ++t) acc[r][t] += __shfl_xor(acc[r][t], off);
+    // lane t (t < T) writes token t of every row
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        if (row >= p.O || lane >= p.T || lane >= TV) continue;
         float v = 0.0f;
 #pragma unroll
         for (int t = 0; t < TV; ++t)
-            if (t == lr) v = acc[t];
-        uint16_t* dst = p.Y + (int64_t)lr * p.O + row;
-        float r = p.alpha * v;
-        if (p.beta != 0.0f) r = fmaf(p.beta, h2f(*dst), r);
-        *dst = f2h(r);
+            if (t == lane) v = acc[r][t];
+        uint16_t* dst = p.Y + (int64_t)lane * p.O + row;
+        float y = p.alpha * v;
+        if (p.beta != 0.0f) y = fmaf(p.beta, h2f(*dst), y);
+        *dst = f2h(y);
     }
 }
 
@@ -168,18 +205,51 @@ namespace {
 
 constexpr size_t kMaxGemvLds = 150 * 1024;
 
-template <int TV>
-clove_status_t run_gemv(const GemvParams& p, bool aligned, hipStream_t stream) {
-    constexpr int LPR = 32;
+// Rows per wave RPW and waves per workgroup: as many chunk loads per lane in
+// flight as fit (8), then enough workgroups to cover every CU.
+struct GemvShape {
+    int rpw, upr, wpb;
+};
+inline GemvShape gemv_shape(int rows, int nch, int cus) {
+    const int cpl = cdiv(nch, 64);
+    GemvShape g{1, 8, 16};
+    if (cpl >= 7) g = {1, 8, 16};
+    else if (cpl >= 5) g = {1, 6, 16};
+    else if (cpl >= 3) g = {2, 4, 16};
+    else if (cpl == 2) g = {4, 2, 16};
+    else g = {8, 1, 16};
+    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
+    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < cus) { g.rpw >>= 1; g.upr <<= 1; }
+    if (g.upr > 8) g.upr = 8;
+    return g;
+}
+
+template <int TV, int RPW, int UPR>
+clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(TV, p.nch);
-    const dim3 grid(cdiv(p.O, 256 / LPR));
-    auto k = aligned ? w4a16_gemv<TV, LPR, true> : w4a16_gemv<TV, LPR, false>;
+    const dim3 grid(cdiv(p.O, wpb * RPW));
+    auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true> : w4a16_gemv<TV, RPW, UPR, false>;
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, grid, dim3(256), lds, stream, p);
+    hipLaunchKernelGGL(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
+}
+
+template <int TV>
+clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    const GemvShape g = gemv_shape(p.O, p.nch, cus);
+    // (rpw, upr) pairs keep rpw * upr <= 8 chunk loads per lane
+    if (g.rpw == 1) {
+        if (g.upr >= 8) return run_gemv_shape<TV, 1, 8>(p, g.wpb, aligned, stream);
+        if (g.upr >= 6) return run_gemv_shape<TV, 1, 6>(p, g.wpb, aligned, stream);
+        if (g.upr >= 4) return run_gemv_shape<TV, 1, 4>(p, g.wpb, aligned, stream);
+        return run_gemv_shape<TV, 1, 2>(p, g.wpb, aligned, stream);
+    }
+    if (g.rpw == 2) return run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return run_gemv_shape<TV, 4, 2>(p, g.wpb, aligned, stream);
+    return run_gemv_shape<TV, 8, 1>(p, g.wpb, aligned, stream);
 }
 
 using mg::Tile;
@@ -222,9 +292,9 @@ clove_status_t launch_w4a16(const W4A16Args& a, hipStream_t stream) {
     if (a.K > 0 && a.T <= 4 && gemv_lds_bytes(tv, nch) <= kMaxGemvLds) {
         GemvParams p{a.X, a.W, a.scale, a.zero, a.Y, a.T, a.O, a.K, G, nch, a.alpha, a.beta};
         const bool aligned = aligned16(a.W) && (a.K % 32 == 0);
-        if (tv == 1) return run_gemv<1>(p, aligned, stream);
-        if (tv == 2) return run_gemv<2>(p, aligned, stream);
-        return run_gemv<4>(p, aligned, stream);
+        if (tv == 1) return run_gemv<1>(p, aligned, dev.num_cus, stream);
+        if (tv == 2) return run_gemv<2>(p, aligned, dev.num_cus, stream);
+        return run_gemv<4>(p, aligned, dev.num_cus, stream);
     }
     mg::Params p{};
     p.a = a.X;
