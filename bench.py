@@ -5,17 +5,24 @@ Headline workload (the step): one FP16 GEMM C = A @ B at M = N = K = 4096,
 row-major, A ~ N(0,1) activations and B ~ N(0,0.02) weights from a fixed
 seed, fp32 accumulation, fp16 output, through the C ABI (clove_gemm_fp16).
 `value` is TFLOP/s = 2*M*N*K / (time per step), inputs resident in HBM, W
-untimed warm-up steps then exactly K timed steps between device syncs.
+untimed warm-up steps then exactly K timed steps between device syncs, HIP
+events on the stream every call is launched on (torch's current stream).
 
 The same JSON line also carries:
-  roofline      the dominant kernel against MI355X dense FP16 MFMA peak
+  roofline      the headline kernel against MI355X dense FP16 MFMA peak, with
+                the HBM traffic per launch from the committed rocprof counters
   cpu_baseline  the oracle's restatement of the reference's naive GEMM
                 (fp32 sequential-k FMA), single thread, on a bounded row sample
   decode        the HBM-bound decode shapes (FP16 1x4096x4096, INT4 W4A4
-                4096x11008 N=1, INT8 1x4096x4096, W4A16 Llama-1B layer at T=1),
-                timed cold: operands rotate through >= 512 MiB of copies so no
-                call finds its operands in the 256 MB Infinity Cache
+                4096x11008 and 11008x4096 at N=1, INT8 1x4096x4096, W4A16
+                Llama-1B layer at T=1)
   prefill       MFMA-bound companions (INT4 N=128, W4A16 layer at T=512)
+Decode and prefill shapes are timed as HIP-graph replays of one call per
+operand copy: the copies rotate through >= 512 MiB so that no call finds its
+operands in the 256 MB Infinity Cache (cold), and the graph removes the
+per-call host launch cost, which exceeds these kernels' run time.  Each graph
+is checked once against the same calls run eagerly.  `us` is graph time per
+call (kernel plus the inter-kernel gap); `us_hot` replays one copy.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
 """
@@ -34,6 +41,7 @@ if ROOT not in sys.path:
 PEAK_FP16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 flop/clk/CU (dense, no sparsity)
 PEAK_INT8_TOPS = 5033.2
 PEAK_HBM_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
 
 
 def parse():
@@ -68,6 +76,45 @@ class Timer:
         self.e.record()
         t.cuda.synchronize()
         return self.s.elapsed_time(self.e) / steps  # ms per call
+
+
+def graph_time(calls, outputs, replays=5):
+    """Captures calls[0..n) into one HIP graph on a private stream (after an
+    eager pass on that stream, which also allocates any split-K scratch for it)
+    and returns the mean time per call in microseconds over `replays` replays.
+    The first replay's outputs must equal the eager ones bit for bit (the
+    kernels are deterministic)."""
+    import torch
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()  # operands were generated on the default stream
+    with torch.cuda.stream(s):
+        for c in calls:
+            c()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outputs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for c in calls:
+            c()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        for o in outputs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outputs, eager):
+            if not torch.equal(o.view(torch.int16), e.view(torch.int16)):
+                raise RuntimeError("graph replay differs from the eager calls")
+        g.replay()
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * len(calls))
+    del g
+    return us
 
 
 def headline(args, timer):
@@ -117,19 +164,16 @@ def cpu_baseline(h, seconds):
                 parity_rows_ok=bool(ok))
 
 
-def rotating(make, nbytes_each, min_total=512 << 20):
-    copies = max(2, -(-min_total // max(1, nbytes_each)))
-    return [make(i) for i in range(copies)]
+def copies_for(nbytes):
+    return max(2, -(-ROTATE_BYTES // max(1, nbytes)))
 
 
-def extras(args, timer):
+def extras():
     import torch
 
     import clove_compute_amd as cg
 
-    res = {}
     gen = torch.Generator(device="cuda")
-    steps, warm = max(args.steps, 100), max(args.warmup, 10)
 
     def f16(shape, scale, seed):
         gen.manual_seed(seed)
@@ -147,76 +191,85 @@ def extras(args, timer):
         gen.manual_seed(seed)
         return torch.randint(0, 16, shape, generator=gen, device="cuda").half()
 
+    def entry(us, nbytes, flops=None, us_hot=None):
+        d = dict(us=us, GBs=nbytes / us / 1e3, frac_hbm=nbytes / us / 1e3 / PEAK_HBM_GBS)
+        if flops is not None:
+            d["TFLOPs"] = flops / us / 1e6
+            d["frac_mfma"] = flops / us / 1e6 / PEAK_FP16_TFLOPS
+        if us_hot is not None:
+            d["us_hot"] = us_hot
+        return d
+
+    dec, pre = {}, {}
+
     # FP16 decode 1x4096x4096 (B is the 32 MiB weight)
     M, N, K = 1, 4096, 4096
     x = f16((M, K), 1.0, 1)
-    Bs = rotating(lambda i: f16((K, N), 0.02, 100 + i), K * N * 2)
-    C = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    ms = timer.run(lambda i: cg.gemm_fp16(x, Bs[i % len(Bs)], C, M, N, K), steps, warm)
-    by = 2 * (M * K + K * N + M * N)
-    res["fp16_1x4096x4096"] = dict(us=ms * 1e3, GBs=by / ms / 1e6, frac_hbm=by / ms / 1e6 / PEAK_HBM_GBS,
-                                   TFLOPs=2 * M * N * K / ms / 1e9)
-    hot = timer.run(lambda i: cg.gemm_fp16(x, Bs[0], C, M, N, K), steps, warm)
-    res["fp16_1x4096x4096"]["us_hot_cache"] = hot * 1e3
-    del Bs
+    nb = 2 * (M * K + K * N + M * N)
+    Bs = [f16((K, N), 0.02, 100 + i) for i in range(copies_for(K * N * 2))]
+    Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
+    calls = [lambda B=B, C=C: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
+    us = graph_time(calls, Cs)
+    hot = graph_time(calls[:1] * 16, Cs[:1])
+    dec["fp16_1x4096x4096"] = entry(us, nb, 2 * M * N * K, hot)
+    del Bs, Cs, calls
 
-    # INT4 W4A4 decode: A_q [4096, 11008/2], N = 1
+    # INT4 W4A4 decode, A_q [M, K/2] group-wise, N = 1
     for (M, K) in ((4096, 11008), (11008, 4096)):
         N, G = 1, -(-K // 128)
-        sets = rotating(lambda i: (u8((M, K // 2), 200 + i), uni16((M, G), 0.001, 0.02, 300 + i),
-                                   zeros16((M, G), 400 + i)), M * K // 2 + 4 * M * G)
+        nb = M * K // 2 + 4 * M * G + K * 1 + 4 * G * N + 2 * M * N
+        sets = [(u8((M, K // 2), 200 + i), uni16((M, G), 0.001, 0.02, 300 + i), zeros16((M, G), 400 + i))
+                for i in range(copies_for(M * K // 2 + 4 * M * G))]
         Bq = u8((K, 1), 5, 16) << 4
         Bsc = uni16((G, N), 0.001, 0.02, 6)
         Bz = zeros16((G, N), 7)
-        C = torch.empty(M, N, dtype=torch.float16, device="cuda")
-        ms = timer.run(lambda i: cg.gemm_int4(*sets[i % len(sets)], Bq, Bsc, Bz, C, M, N, K), steps, warm)
-        by = M * K // 2 + 4 * M * G + K * 1 + 4 * G * N + 2 * M * N
-        res[f"int4_w4a4_{M}x{K}_n1"] = dict(us=ms * 1e3, GBs=by / ms / 1e6,
-                                             frac_hbm=by / ms / 1e6 / PEAK_HBM_GBS)
-        hot = timer.run(lambda i: cg.gemm_int4(sets[0][0], sets[0][1], sets[0][2], Bq, Bsc, Bz, C, M, N, K),
-                        steps, warm)
-        res[f"int4_w4a4_{M}x{K}_n1"]["us_hot_cache"] = hot * 1e3
-        del sets
+        Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in sets]
+        calls = [lambda s=s, C=C: cg.gemm_int4(*s, Bq, Bsc, Bz, C, M, N, K) for s, C in zip(sets, Cs)]
+        us = graph_time(calls, Cs)
+        hot = graph_time(calls[:1] * 16, Cs[:1])
+        dec[f"int4_w4a4_{M}x{K}_n1"] = entry(us, nb, None, hot)
+        del sets, Cs, calls
 
     # INT8 W8A8 decode 1x4096x4096 with per-row / per-column scales
     M, N, K = 1, 4096, 4096
     a8 = u8((M, K), 8).view(torch.int8)
-    Bs = rotating(lambda i: u8((K, N), 500 + i).view(torch.int8), K * N)
     sa = uni16((M,), 0.001, 0.02, 9)
     sb = uni16((N,), 0.001, 0.02, 10)
-    C = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    ms = timer.run(lambda i: cg.gemm_int8_rowcol(a8, Bs[i % len(Bs)], sa, sb, C, M, N, K), steps, warm)
-    by = M * K + K * N + 2 * M * N + 2 * M + 2 * N
-    res["int8_1x4096x4096"] = dict(us=ms * 1e3, GBs=by / ms / 1e6, frac_hbm=by / ms / 1e6 / PEAK_HBM_GBS)
-    del Bs
+    nb = M * K + K * N + 2 * M * N + 2 * M + 2 * N
+    Bs = [u8((K, N), 500 + i).view(torch.int8) for i in range(copies_for(K * N))]
+    Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
+    calls = [lambda B=B, C=C: cg.gemm_int8_rowcol(a8, B, sa, sb, C, M, N, K) for B, C in zip(Bs, Cs)]
+    us = graph_time(calls, Cs)
+    dec["int8_1x4096x4096"] = entry(us, nb)
+    del Bs, Cs, calls
 
-    # W4A16 Llama-1B decoder-layer GEMM sequence (QKV, O+res, gate, up, down+res)
-    layer = [(3072, 2048, 0.0), (2048, 2048, 1.0), (8192, 2048, 0.0), (8192, 2048, 0.0),
-             (2048, 8192, 1.0)]
+    # W4A16 Llama-1B decoder-layer GEMM sequence (QKV, O + residual, gate, up, down + residual)
+    layer = [(3072, 2048, 0.0), (2048, 2048, 1.0), (8192, 2048, 0.0), (8192, 2048, 0.0), (2048, 8192, 1.0)]
+    wbytes = sum(O * K // 2 + 4 * O * (-(-K // 128)) for O, K, _ in layer)
 
     def make_layer(i):
         return [(u8((O, K // 2), 600 + 10 * i + j), uni16((O, -(-K // 128)), 0.001, 0.02, 700 + 10 * i + j),
                  zeros16((O, -(-K // 128)), 800 + 10 * i + j)) for j, (O, K, _) in enumerate(layer)]
 
-    wbytes = sum(O * K // 2 + 4 * O * (-(-K // 128)) for O, K, _ in layer)
     for T in (1, 512):
-        layers = rotating(make_layer, wbytes) if T == 1 else [make_layer(0)]
+        layers = [make_layer(i) for i in range(copies_for(wbytes) if T == 1 else 2)]
         xs = [f16((T, K), 1.0, 900 + j) for j, (O, K, _) in enumerate(layer)]
         ys = [f16((T, O), 1.0, 950 + j) for j, (O, K, _) in enumerate(layer)]
 
-        def step(i, layers=layers, xs=xs, ys=ys, T=T):
-            L = layers[i % len(layers)]
+        def step(L, xs=xs, ys=ys, T=T):
             for j, (O, K, beta) in enumerate(layer):
                 w, s, z = L[j]
                 cg.gemm_w4a16(xs[j], w, s, z, ys[j], T, O, K, 1.0, beta)
 
-        ms = timer.run(step, steps if T == 1 else max(20, args.steps // 2), warm)
+        # the residual projections accumulate into ys across calls: compare the
+        # non-residual outputs only
+        check = [ys[0], ys[2], ys[3]]
+        calls = [lambda L=L: step(L) for L in layers]
+        us = graph_time(calls, check, replays=5 if T == 1 else 3)
         flops = sum(2 * T * O * K for O, K, _ in layer)
-        by = wbytes + sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
-        key = f"w4a16_llama1b_layer_T{T}"
-        res[key] = dict(us=ms * 1e3, TFLOPs=flops / ms / 1e9, GBs=by / ms / 1e6,
-                        frac_hbm=by / ms / 1e6 / PEAK_HBM_GBS, frac_mfma=flops / ms / 1e9 / PEAK_FP16_TFLOPS)
-        del layers
+        nb = wbytes + sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
+        (dec if T == 1 else pre)[f"w4a16_llama1b_layer_T{T}"] = entry(us, nb, flops)
+        del layers, calls
 
     # INT4 W4A4 N=128 (MFMA side of config 4)
     M, N, K = 4096, 128, 11008
@@ -224,11 +277,11 @@ def extras(args, timer):
     Aq, As, Az = u8((M, K // 2), 11), uni16((M, G), 0.001, 0.02, 12), zeros16((M, G), 13)
     Bq, Bsc, Bz = u8((K, N // 2), 14), uni16((G, N), 0.001, 0.02, 15), zeros16((G, N), 16)
     C = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    ms = timer.run(lambda i: cg.gemm_int4(Aq, As, Az, Bq, Bsc, Bz, C, M, N, K), steps, warm)
-    by = M * K // 2 + 4 * M * G + K * N // 2 + 4 * G * N + 2 * M * N
-    res["int4_w4a4_4096x11008_n128"] = dict(us=ms * 1e3, TFLOPs=2 * M * N * K / ms / 1e9, GBs=by / ms / 1e6,
-                                            frac_hbm=by / ms / 1e6 / PEAK_HBM_GBS)
-    return res
+    calls = [lambda: cg.gemm_int4(Aq, As, Az, Bq, Bsc, Bz, C, M, N, K)] * 8
+    us = graph_time(calls, [C], replays=3)
+    nb = M * K // 2 + 4 * M * G + K * N // 2 + 4 * G * N + 2 * M * N
+    pre["int4_w4a4_4096x11008_n128"] = entry(us, nb, 2 * M * N * K)
+    return dec, pre
 
 
 def main():
@@ -271,14 +324,13 @@ def main():
                    "layout": "row-major A[M,K] B[K,N] C[M,N]", "accumulate": "fp32"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                     "traffic": traffic, "flops_per_launch": flops},
+                     "traffic": traffic, "flops_per_launch": flops,
+                     "kernel": "dma::gemm_f16_dma<Cfg<256,256,64,2,2>>"},
     }
     if not args.skip_extra:
-        ex = extras(args, timer)
-        line["decode"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in ex.items()
-                          if "n128" not in k and "T512" not in k}
-        line["prefill"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in ex.items()
-                           if "n128" in k or "T512" in k}
+        dec, pre = extras()
+        line["decode"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in dec.items()}
+        line["prefill"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in pre.items()}
     if args.cpu_seconds > 0:
         cb = cpu_baseline(h, args.cpu_seconds)
         cb["value"] = round(cb["value"], 6)
