@@ -13,16 +13,18 @@ The same JSON line also carries:
                 the HBM traffic per launch from the committed rocprof counters
   cpu_baseline  the oracle's restatement of the reference's naive GEMM
                 (fp32 sequential-k FMA), single thread, on a bounded row sample
-  decode        the HBM-bound decode shapes (FP16 1x4096x4096, INT4 W4A4
-                4096x11008 and 11008x4096 at N=1, INT8 1x4096x4096, W4A16
-                Llama-1B layer at T=1)
-  prefill       MFMA-bound companions (INT4 N=128, W4A16 layer at T=512)
-Decode and prefill shapes are timed as HIP-graph replays of one call per
-operand copy: the copies rotate through >= 512 MiB so that no call finds its
-operands in the 256 MB Infinity Cache (cold), and the graph removes the
-per-call host launch cost, which exceeds these kernels' run time.  Each graph
-is checked once against the same calls run eagerly.  `us` is graph time per
-call (kernel plus the inter-kernel gap); `us_hot` replays one copy.
+  shapes        every other shape of the five named configurations: FP16 512^3
+                and M = 1/32/128 at 4096x4096, INT8 M = 1/128, INT4 W4A4
+                (11008x4096 and 4096x11008, N = 1/16/128), the W4A16 Llama-1B
+                layer at T = 1 and 512; each with t_roof = max(flops / MFMA
+                peak, bytes / 8 TB/s) and frac_roofline = t_roof / time
+The shapes are timed as HIP-graph replays of one call per operand copy: the
+copies rotate through >= 512 MiB so that no call finds its weights in the
+256 MB Infinity Cache (cold), and the graph removes the per-call host launch
+cost, which exceeds most of these kernels' run time.  Each graph is checked
+once against the same calls run eagerly.  `us` is graph time per call (kernel
+plus the inter-kernel gap); `us_hot` replays one copy.  INT4 W4A4 is priced
+at the INT8 MFMA peak (its integer products fit i8 operands).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
 """
@@ -169,6 +171,8 @@ def copies_for(nbytes):
 
 
 def extras():
+    """Every shape of the five named configurations except the headline, each
+    timed as graph replays with cold weights.  Returns {name: figures}."""
     import torch
 
     import clove_compute_amd as cg
@@ -179,9 +183,17 @@ def extras():
         gen.manual_seed(seed)
         return (torch.randn(shape, generator=gen, device="cuda") * scale).half()
 
+    def u16(shape, seed):  # fp16 ~U[-1, 1]
+        gen.manual_seed(seed)
+        return (torch.rand(shape, generator=gen, device="cuda") * 2 - 1).half()
+
     def u8(shape, seed, hi=256):
         gen.manual_seed(seed)
         return torch.randint(0, hi, shape, generator=gen, device="cuda", dtype=torch.uint8)
+
+    def i8(shape, seed):
+        gen.manual_seed(seed)
+        return torch.randint(-127, 128, shape, generator=gen, device="cuda", dtype=torch.int8)
 
     def uni16(shape, lo, hi, seed):
         gen.manual_seed(seed)
@@ -191,59 +203,67 @@ def extras():
         gen.manual_seed(seed)
         return torch.randint(0, 16, shape, generator=gen, device="cuda").half()
 
-    def entry(us, nbytes, flops=None, us_hot=None):
-        d = dict(us=us, GBs=nbytes / us / 1e3, frac_hbm=nbytes / us / 1e3 / PEAK_HBM_GBS)
-        if flops is not None:
-            d["TFLOPs"] = flops / us / 1e6
-            d["frac_mfma"] = flops / us / 1e6 / PEAK_FP16_TFLOPS
-        if us_hot is not None:
-            d["us_hot"] = us_hot
-        return d
+    out = {}
 
-    dec, pre = {}, {}
+    def record(name, calls, outputs, flops, nbytes, peak, hot_calls=None, replays=5):
+        us = graph_time(calls, outputs, replays)
+        t_mfma = flops / (peak * 1e6)
+        t_hbm = nbytes / (PEAK_HBM_GBS * 1e3)
+        t_roof = max(t_mfma, t_hbm)
+        d = dict(us=us, TFLOPs=flops / us / 1e6, GBs=nbytes / us / 1e3,
+                 bound="mfma" if t_mfma >= t_hbm else "hbm", t_roof_us=t_roof, frac_roofline=t_roof / us)
+        if hot_calls is not None:
+            d["us_hot"] = graph_time(hot_calls, outputs[:1], replays)
+        out[name] = d
 
-    # FP16 decode 1x4096x4096 (B is the 32 MiB weight)
-    M, N, K = 1, 4096, 4096
-    x = f16((M, K), 1.0, 1)
-    nb = 2 * (M * K + K * N + M * N)
-    Bs = [f16((K, N), 0.02, 100 + i) for i in range(copies_for(K * N * 2))]
-    Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
-    calls = [lambda B=B, C=C: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
-    us = graph_time(calls, Cs)
-    hot = graph_time(calls[:1] * 16, Cs[:1])
-    dec["fp16_1x4096x4096"] = entry(us, nb, 2 * M * N * K, hot)
-    del Bs, Cs, calls
+    # ---- FP16: 512^3 (U[-1,1]) and the decode/prefill rows of the LLM shapes ----
+    A5, B5 = u16((512, 512), 1), u16((512, 512), 2)
+    C5 = torch.empty(512, 512, dtype=torch.float16, device="cuda")
+    c = [lambda: cg.gemm_fp16(A5, B5, C5, 512, 512, 512)] * 16
+    record("fp16_512x512x512", c, [C5], 2 * 512 ** 3, 2 * 3 * 512 * 512, PEAK_FP16_TFLOPS)
+    for M in (1, 32, 128):
+        N = K = 4096
+        x = f16((M, K), 1.0, 3 + M)
+        Bs = [f16((K, N), 0.02, 100 + i) for i in range(copies_for(K * N * 2))]
+        Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
+        calls = [lambda B=B, C=C, M=M: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
+        record(f"fp16_{M}x4096x4096", calls, Cs, 2 * M * N * K, 2 * (M * K + K * N + M * N),
+               PEAK_FP16_TFLOPS, hot_calls=calls[:1] * 16 if M == 1 else None)
+        del Bs, Cs, calls
 
-    # INT4 W4A4 decode, A_q [M, K/2] group-wise, N = 1
-    for (M, K) in ((4096, 11008), (11008, 4096)):
-        N, G = 1, -(-K // 128)
-        nb = M * K // 2 + 4 * M * G + K * 1 + 4 * G * N + 2 * M * N
+    # ---- INT8 W8A8 with per-row / per-column fp16 scales ----
+    for M in (1, 128):
+        N = K = 4096
+        a8 = i8((M, K), 8 + M)
+        sa = uni16((M,), 0.001, 0.02, 9)
+        sb = uni16((N,), 0.001, 0.02, 10)
+        Bs = [i8((K, N), 500 + i) for i in range(copies_for(K * N))]
+        Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
+        calls = [lambda B=B, C=C, M=M: cg.gemm_int8_rowcol(a8, B, sa, sb, C, M, N, K) for B, C in zip(Bs, Cs)]
+        record(f"int8_{M}x4096x4096", calls, Cs, 2 * M * N * K, M * K + K * N + 2 * M * N + 2 * M + 2 * N,
+               PEAK_INT8_TOPS)
+        del Bs, Cs, calls
+
+    # ---- INT4 W4A4 group-wise: weights A_q [M, K/2], activations B_q [K, ceil(N/2)] ----
+    for (M, K) in ((11008, 4096), (4096, 11008)):
+        G = -(-K // 128)
+        wbytes = M * K // 2 + 4 * M * G
         sets = [(u8((M, K // 2), 200 + i), uni16((M, G), 0.001, 0.02, 300 + i), zeros16((M, G), 400 + i))
-                for i in range(copies_for(M * K // 2 + 4 * M * G))]
-        Bq = u8((K, 1), 5, 16) << 4
-        Bsc = uni16((G, N), 0.001, 0.02, 6)
-        Bz = zeros16((G, N), 7)
-        Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in sets]
-        calls = [lambda s=s, C=C: cg.gemm_int4(*s, Bq, Bsc, Bz, C, M, N, K) for s, C in zip(sets, Cs)]
-        us = graph_time(calls, Cs)
-        hot = graph_time(calls[:1] * 16, Cs[:1])
-        dec[f"int4_w4a4_{M}x{K}_n1"] = entry(us, nb, None, hot)
-        del sets, Cs, calls
+                for i in range(copies_for(wbytes))]
+        for N in (1, 16, 128):
+            Bq = u8((K, 1), 5, 16) << 4 if N == 1 else u8((K, (N + 1) // 2), 5)
+            Bsc = uni16((G, N), 0.001, 0.02, 6)
+            Bz = zeros16((G, N), 7)
+            Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in sets]
+            calls = [lambda s=s, C=C, Bq=Bq, Bsc=Bsc, Bz=Bz, N=N: cg.gemm_int4(*s, Bq, Bsc, Bz, C, M, N, K)
+                     for s, C in zip(sets, Cs)]
+            nb = wbytes + K * ((N + 1) // 2) + 4 * G * N + 2 * M * N
+            record(f"int4_w4a4_{M}x{K}_n{N}", calls, Cs, 2 * M * N * K, nb, PEAK_INT8_TOPS,
+                   hot_calls=calls[:1] * 16 if N == 1 else None)
+            del Cs, calls
+        del sets
 
-    # INT8 W8A8 decode 1x4096x4096 with per-row / per-column scales
-    M, N, K = 1, 4096, 4096
-    a8 = u8((M, K), 8).view(torch.int8)
-    sa = uni16((M,), 0.001, 0.02, 9)
-    sb = uni16((N,), 0.001, 0.02, 10)
-    nb = M * K + K * N + 2 * M * N + 2 * M + 2 * N
-    Bs = [u8((K, N), 500 + i).view(torch.int8) for i in range(copies_for(K * N))]
-    Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
-    calls = [lambda B=B, C=C: cg.gemm_int8_rowcol(a8, B, sa, sb, C, M, N, K) for B, C in zip(Bs, Cs)]
-    us = graph_time(calls, Cs)
-    dec["int8_1x4096x4096"] = entry(us, nb)
-    del Bs, Cs, calls
-
-    # W4A16 Llama-1B decoder-layer GEMM sequence (QKV, O + residual, gate, up, down + residual)
+    # ---- W4A16 Llama-1B decoder-layer GEMM sequence (QKV, O + residual, gate, up, down + residual) ----
     layer = [(3072, 2048, 0.0), (2048, 2048, 1.0), (8192, 2048, 0.0), (8192, 2048, 0.0), (2048, 8192, 1.0)]
     wbytes = sum(O * K // 2 + 4 * O * (-(-K // 128)) for O, K, _ in layer)
 
@@ -263,25 +283,13 @@ def extras():
 
         # the residual projections accumulate into ys across calls: compare the
         # non-residual outputs only
-        check = [ys[0], ys[2], ys[3]]
         calls = [lambda L=L: step(L) for L in layers]
-        us = graph_time(calls, check, replays=5 if T == 1 else 3)
         flops = sum(2 * T * O * K for O, K, _ in layer)
         nb = wbytes + sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
-        (dec if T == 1 else pre)[f"w4a16_llama1b_layer_T{T}"] = entry(us, nb, flops)
+        record(f"w4a16_llama1b_layer_T{T}", calls, [ys[0], ys[2], ys[3]], flops, nb, PEAK_FP16_TFLOPS,
+               replays=5 if T == 1 else 3)
         del layers, calls
-
-    # INT4 W4A4 N=128 (MFMA side of config 4)
-    M, N, K = 4096, 128, 11008
-    G = -(-K // 128)
-    Aq, As, Az = u8((M, K // 2), 11), uni16((M, G), 0.001, 0.02, 12), zeros16((M, G), 13)
-    Bq, Bsc, Bz = u8((K, N // 2), 14), uni16((G, N), 0.001, 0.02, 15), zeros16((G, N), 16)
-    C = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    calls = [lambda: cg.gemm_int4(Aq, As, Az, Bq, Bsc, Bz, C, M, N, K)] * 8
-    us = graph_time(calls, [C], replays=3)
-    nb = M * K // 2 + 4 * M * G + K * N // 2 + 4 * G * N + 2 * M * N
-    pre["int4_w4a4_4096x11008_n128"] = entry(us, nb, 2 * M * N * K)
-    return dec, pre
+    return out
 
 
 def main():
@@ -328,9 +336,8 @@ def main():
                      "kernel": "dma::gemm_f16_dma<Cfg<256,256,64,2,2>>"},
     }
     if not args.skip_extra:
-        dec, pre = extras()
-        line["decode"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in dec.items()}
-        line["prefill"] = {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in pre.items()}
+        line["shapes"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                          for k, v in extras().items()}
     if args.cpu_seconds > 0:
         cb = cpu_baseline(h, args.cpu_seconds)
         cb["value"] = round(cb["value"], 6)

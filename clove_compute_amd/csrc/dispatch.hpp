@@ -77,6 +77,13 @@ struct W4A16Args {
 };
 clove_status_t launch_w4a16(const W4A16Args& args, hipStream_t stream);
 
+// MFMA path for INT4 weight rows x fp16 activations (i4w_gemm.hip).  Each
+// returns false, launching nothing, when the shape or alignment is outside
+// what the kernel handles (the caller then takes its general path); otherwise
+// it launches and stores the launch status in *status.
+bool try_i4w_w4a16(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+bool try_i4w_int4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+
 inline clove_status_t check_launch() {
     return hipGetLastError() == hipSuccess ? CLOVE_OK : CLOVE_ERR_LAUNCH;
 }

@@ -424,6 +424,10 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
         return literal ? gemv_by_n<mg::kI4Literal>(p, aligned, dev.num_cus, stream)
                        : gemv_by_n<mg::kI4Groupwise>(p, aligned, dev.num_cus, stream);
     }
+    if (!literal) {
+        clove_status_t st2;
+        if (try_i4w_int4(a, dev.num_cus, stream, &st2)) return st2;
+    }
     mg::Params p{};
     p.a = a.A; p.a_scale = a.A_scale; p.a_zero = a.A_zero;
     p.b = a.B; p.b_scale = a.B_scale; p.b_zero = a.B_zero;

@@ -1,0 +1,139 @@
+// Host side of the INT4-weight MFMA GEMM (i4w_gemm.hpp): tile configuration,
+// split-K plan, scratch, and the B transpose of group-wise INT4.
+#include "dispatch.hpp"
+#include "i4w_gemm.hpp"
+
+namespace clove {
+namespace {
+
+using namespace i4w;
+
+// (WR, WC, FW, FX, stages): waves along weight rows x along X rows, 32x32
+// tiles per wave in each direction
+using CfgBig = Cfg<4, 1, 2, 4, 3>;  // 256 x 128, 4 waves of 64 x 128
+using CfgSq = Cfg<2, 2, 2, 2, 3>;   // 128 x 128, 4 waves of 64 x 64
+using CfgC64 = Cfg<4, 1, 1, 2, 3>;  // 128 x 64
+using CfgC32 = Cfg<2, 1, 1, 1, 4>;  // 64 x 32, 2 waves (several workgroups per CU)
+
+inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct Plan {
+    int tiles_r, tiles_c, nsplit, gps;
+};
+
+// split K (whole groups, at least two per split) until the grid reaches `target`
+template <class CF>
+Plan make_plan(int R, int C, int G, int target) {
+    Plan pl;
+    pl.tiles_r = cdiv(R, CF::BR);
+    pl.tiles_c = cdiv(C, CF::BC);
+    const int tiles = pl.tiles_r * pl.tiles_c;
+    int ns = tiles >= target ? 1 : target / tiles;
+    ns = max(1, min(ns, G / 2));
+    pl.gps = cdiv(G, ns);
+    pl.nsplit = cdiv(G, pl.gps);
+    return pl;
+}
+
+// `prep(args, extra)` runs before the GEMM with `extra_bytes` of scratch
+// (after the split-K partials) and may point args.X / args.xs into it
+template <class CF, bool XS, int OUT, class Prep>
+clove_status_t run(Args a, int target, size_t extra_bytes, hipStream_t stream, Prep prep) {
+    const Plan pl = make_plan<CF>(a.R, a.C, a.G, target);
+    a.tiles_r = pl.tiles_r;
+    a.tiles_c = pl.tiles_c;
+    a.nsplit = pl.nsplit;
+    a.gps = pl.gps;
+    const int tiles = pl.tiles_r * pl.tiles_c;
+    const size_t part_bytes =
+        pl.nsplit > 1 ? round256((size_t)tiles * pl.nsplit * CF::NT * CF::FW * CF::FX * 16 * sizeof(float)) : 0;
+    char* extra = nullptr;
+    if (part_bytes + extra_bytes > 0) {
+        Scratch s;
+        const clove_status_t st = acquire_scratch(stream, part_bytes + extra_bytes, (size_t)tiles, &s);
+        if (st != CLOVE_OK) return st;
+        a.part = s.partials;
+        a.counters = s.counters;
+        extra = reinterpret_cast<char*>(s.partials) + part_bytes;
+    }
+    const clove_status_t st = prep(a, extra);
+    if (st != CLOVE_OK) return st;
+    auto k = i4w_gemm<CF, XS, OUT>;
+    constexpr int lds = CF::template lds_bytes<XS>();
+    static_assert(lds <= 160 * 1024, "LDS");
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            lds) != hipSuccess)
+        return CLOVE_ERR_LAUNCH;
+    hipLaunchKernelGGL(k, dim3((unsigned)(tiles * pl.nsplit)), dim3(CF::NT), lds, stream, a);
+    return check_launch();
+}
+
+template <bool XS, int OUT, class Prep>
+clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t stream, Prep prep) {
+    if (a.C <= 32) return run<CfgC32, XS, OUT>(a, 2 * cus, extra_bytes, stream, prep);
+    if (a.C <= 64) return run<CfgC64, XS, OUT>(a, cus, extra_bytes, stream, prep);
+    if (cdiv(a.R, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= cus)
+        return run<CfgBig, XS, OUT>(a, cus, extra_bytes, stream, prep);
+    return run<CfgSq, XS, OUT>(a, cus, extra_bytes, stream, prep);
+}
+
+bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
+
+}  // namespace
+
+bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status_t* status) {
+    if (w.T <= 4 || w.K <= 0 || w.K % 128 != 0 || !aligned16(w.X) || !aligned16(w.W)) return false;
+    if (!fits31((int64_t)w.T * w.K * 2) || !fits31((int64_t)w.O * (w.K / 2))) return false;
+    Args a{};
+    a.W = w.W;
+    a.wscale = w.scale;
+    a.wzero = w.zero;
+    a.X = w.X;
+    a.out = w.Y;
+    a.R = w.O;
+    a.C = w.T;
+    a.K = w.K;
+    a.G = w.K / 128;
+    a.alpha = w.alpha;
+    a.beta = w.beta;
+    *status = by_shape<false, 1>(a, cus, 0, stream, [](Args&, char*) { return CLOVE_OK; });
+    return true;
+}
+
+bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t* status) {
+    if (q.mode != CLOVE_INT4_GROUPWISE || q.N <= 8 || q.K <= 0 || q.K % 128 != 0 || !aligned16(q.A))
+        return false;
+    const int Npad = (q.N + 63) / 64 * 64;
+    const int G = q.K / 128;
+    if (!fits31((int64_t)Npad * q.K * 2) || !fits31((int64_t)q.M * (q.K / 2))) return false;
+    const size_t xt_bytes = round256((size_t)Npad * q.K * 2);
+    const size_t xs_bytes = round256((size_t)G * Npad * 4);
+    Args a{};
+    a.W = q.A;
+    a.wscale = q.A_scale;
+    a.wzero = q.A_zero;
+    a.out = q.C;
+    a.R = q.M;
+    a.C = q.N;
+    a.K = q.K;
+    a.G = G;
+    a.ldxs = Npad;
+    a.alpha = 1.0f;
+    a.beta = 0.0f;
+    const int ldb = (q.N + 1) / 2;
+    auto prep = [&](Args& args, char* extra) -> clove_status_t {
+        uint16_t* xt = reinterpret_cast<uint16_t*>(extra);
+        float* xs = reinterpret_cast<float*>(extra + xt_bytes);
+        const int64_t threads = (int64_t)(q.K / 8) * (Npad / 2);
+        hipLaunchKernelGGL(i4w_prep_b, dim3((unsigned)cdiv64(threads, 256)), dim3(256), 0, stream, q.B, ldb,
+                           q.B_scale, q.B_zero, q.N, q.K, G, Npad, xt, xs);
+        args.X = xt;
+        args.xs = xs;
+        return check_launch();
+    };
+    *status = by_shape<true, 0>(a, cus, xt_bytes + xs_bytes, stream, prep);
+    return true;
+}
+
+}  // namespace clove

@@ -1,0 +1,457 @@
+// MFMA GEMM with packed INT4 weight rows for gfx950: the prefill shapes of the
+// W4A16 linear layer (T > 4 tokens) and of group-wise INT4 (N > 8 columns).
+//
+//   out[r, c] = sum_g  sw[r,g] * sx[g,c] * P_g[r,c]
+//   P_g[r,c]  = sum_{k in group g} (q[r,k] - zw[r,g]) * x[c,k]
+//
+//   W  [R, K/2]  packed INT4 rows, even k in the high nibble (gemm_int4's A,
+//                W4A16's weight), fp16 group scales sw and zero points zw [R, G]
+//   X  [C, K]    fp16, K-contiguous: W4A16's activations, or for INT4 the
+//                exact integers qB - zB of B transposed (prepared by i4w_prep_b)
+//   sx [G, ldxs] fp32 per-(group, column) scale of X (INT4; absent for W4A16)
+//
+// q - z is exact in fp16 and so is every product with an fp16 x, so P_g is an
+// fp32 MFMA sum of exact products (exact integers for INT4), and each group is
+// folded into the fp32 accumulator with its scale: acc = fma(sw * sx, P_g, acc),
+// the arithmetic of the reference-derived group-wise definition.
+//
+// Nibble unpack (10 VALU ops per 8 weights).  A dword w of packed weights holds
+// k0..k7; hr = w & 0xf0f0f0f0 and lo = w & 0x0f0f0f0f, then one v_perm_b32 per
+// byte b builds the half2 {hr.b, lo.b} with zero high bytes: the fp16
+// subnormals 16 h * 2^-24 and l * 2^-24 (h, l the two nibbles).  One
+// v_pk_fma_f16 by {2^11, 2^15} plus {-z 2^-9, -z 2^-9} gives (h - z) 2^-9 and
+// (l - z) 2^-9, both exact; the 2^-9 is returned through the group scale
+// (sw * 2^9, exact).
+//
+// Tiles.  A workgroup of NW = WR x WC waves owns BR = 32 FW WR weight rows by
+// BC = 32 FX WC X rows; each wave owns (32 FW) x (32 FX) outputs as FW x FX
+// v_mfma_f32_32x32x16_f16 tiles with the X fragment as the MFMA "A" operand
+// and the weight fragment as "B", so a lane holds one weight row r (its scale
+// and zero are per-lane scalars) and 16 X rows.  K advances one 128-wide group
+// per stage.  Split-K over groups when the tiles do not cover the CUs: fp32
+// partial tiles in scratch, the last-arriving workgroup of a tile sums them in
+// split order (deterministic).
+//
+// Staging.  Everything a stage needs arrives by LDS DMA (inline asm, so that
+// the compiler does not wait for all DMAs before each LDS read; completion is
+// tracked with explicit vmcnt waits and one barrier per stage):
+//   X   BC rows x 256 B, 16-byte chunk c of row x at slot c ^ (x & 7)
+//   W   BR rows x 64 B,  chunk c of row r at slot c ^ ((r >> 1) & 3)
+//   SC  BR dwords, the aligned dword holding sw[r, g]   (half chosen by parity)
+//   ZR  BR dwords, the same for zw[r, g]
+//   XS  64 NW fp32 of sx[g, c0 ...]                     (INT4 only)
+// so X fragment reads (ds_read_b128) and weight reads (2 x ds_read_b128 per
+// lane per group: 64 k of its row) are bank-conflict free.  Lane (r, h) of a
+// weight tile covers k = 64 h .. 64 h + 63 of the group and uses dword s of it
+// in k-step s; the X fragment of step s is x[c][64 h + 8 s .. + 7].
+#pragma once
+
+#include "common.hpp"
+#include "f16_dma_gemm.hpp"
+
+namespace clove {
+namespace i4w {
+
+using namespace hw;
+using dma::dma16;
+using dma::make_rsrc;
+using dma::vmcnt_imm;
+
+struct Args {
+    const uint8_t* W;
+    const uint16_t* wscale;  // [R, G] fp16
+    const uint16_t* wzero;   // [R, G] fp16
+    const uint16_t* X;       // [C, K] fp16 (rows >= C read as zero)
+    const float* xs;         // [G, ldxs] fp32 or null
+    uint16_t* out;           // OUT 0: [R, C] (C[m, n]),  OUT 1: [C, R] (Y[t, o])
+    int R, C, K, G, ldxs;
+    float alpha, beta;       // OUT 1 epilogue: alpha * acc + beta * out
+    int tiles_r, tiles_c, nsplit, gps;  // gps: groups per split
+    float* part;
+    unsigned* counters;
+};
+
+template <int WR_, int WC_, int FW_, int FX_, int S_>
+struct Cfg {
+    static constexpr int WR = WR_, WC = WC_, FW = FW_, FX = FX_, S = S_;
+    static constexpr int NW = WR * WC, NT = 64 * NW;
+    static constexpr int BR = 32 * FW * WR, BC = 32 * FX * WC;
+    static constexpr int X_BYTES = BC * 256, W_BYTES = BR * 64, SC_BYTES = BR * 4;
+    static constexpr int DX = BC / (4 * NW);        // X DMA instructions per thread per stage
+    static constexpr int DW = BR / (16 * NW);       // weight DMA instructions
+    static constexpr int DS = 2 * BR / (64 * NW);   // scale + zero DMA instructions
+    static_assert(NW == 2 || NW == 4, "waves");
+    static_assert(BC % (4 * NW) == 0 && BR % (16 * NW) == 0 && (2 * BR) % (64 * NW) == 0, "DMA split");
+    static_assert(BC <= 64 * NW, "one dword of sx per lane covers the tile");
+    static_assert(S >= 2 && S <= 4, "stages");
+    template <bool XS>
+    static constexpr int stage_bytes() { return X_BYTES + W_BYTES + 2 * SC_BYTES + (XS ? 256 * NW : 0); }
+    template <bool XS>
+    static constexpr int lds_bytes() { return S * stage_bytes<XS>(); }
+    template <bool XS>
+    static constexpr int dma_per_stage() { return DX + DW + DS + (XS ? 1 : 0); }
+};
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) unsigned lds_u32;
+
+__device__ __forceinline__ u32x4 lds_read16(unsigned addr) {
+    return *reinterpret_cast<const lds_u32x4*>((size_t)addr);
+}
+__device__ __forceinline__ unsigned lds_read4(unsigned addr) {
+    return *reinterpret_cast<const lds_u32*>((size_t)addr);
+}
+
+__device__ __forceinline__ void dma4(const u32x4& rsrc, unsigned lds_addr, int voff, int soff) {
+    asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
+                 : "memory");
+}
+
+// 16-byte store that is visible device-wide once complete (cache policy sc1:
+// written through past the XCD-private L2), for split-K partials.  A compiler
+// builtin rather than inline asm: the backend must see the store to keep its
+// data registers live until the hardware has read them (a VALU write right
+// after a >8-byte store would otherwise race with it).
+constexpr int kCpolSc1 = 16;
+__device__ __forceinline__ void store16_coherent(__amdgpu_buffer_rsrc_t rsrc, int byte_off, const f32x4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(bitcast<u32x4>(v), rsrc, byte_off, 0, kCpolSc1);
+}
+
+// (q - z) * 2^-9 for the 8 nibbles of one dword, in k order; zz = -z * 2^-9
+__device__ __forceinline__ f16x8 unpack8(unsigned w, f16x2 zz) {
+    const unsigned hr = w & 0xf0f0f0f0u, lo = w & 0x0f0f0f0fu;
+    const f16x2 mul = {(_Float16)2048.0f, (_Float16)32768.0f};
+    f16x2 v[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const unsigned sel = 0x0c000c00u | (unsigned)b | ((unsigned)(4 + b) << 16);
+        const f16x2 sub = bitcast<f16x2>(__builtin_amdgcn_perm(lo, hr, sel));
+        v[b] = __builtin_elementwise_fma(sub, mul, zz);
+    }
+    f16x8 r;
+    r.s01 = v[0];
+    r.s23 = v[1];
+    r.s45 = v[2];
+    r.s67 = v[3];
+    return r;
+}
+
+template <int IMM>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt(IMM);
+}
+
+template <class CF, bool XS, int OUT>
+__global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
+    constexpr int NW = CF::NW, FW = CF::FW, FX = CF::FX, S = CF::S;
+    constexpr int BR = CF::BR, BC = CF::BC;
+    constexpr int SB = CF::template stage_bytes<XS>();
+    constexpr int OFF_W = CF::X_BYTES, OFF_SC = OFF_W + CF::W_BYTES, OFF_ZR = OFF_SC + CF::SC_BYTES,
+                  OFF_XS = OFF_ZR + CF::SC_BYTES;
+    constexpr int D = CF::template dma_per_stage<XS>();
+    extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave % CF::WR, wc = wave / CF::WR;
+
+    // ---- tile, split, K range ----
+    const int bid = blockIdx.x;
+    const int split = bid % p.nsplit;
+    const int tile = bid / p.nsplit;
+    const int tc = tile % p.tiles_c, tr = tile / p.tiles_c;
+    const int r0 = tr * BR, c0 = tc * BC;
+    const int gbeg = split * p.gps;
+    const int nkt = min(p.G, gbeg + p.gps) - gbeg;
+    const int R = p.R, K = p.K, G = p.G;
+
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane(
+        (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char*)smem));
+
+    // ---- DMA descriptors and per-lane offsets (fixed over K) ----
+    const u32x4 rx = make_rsrc(p.X, (unsigned)p.C * K * 2);
+    const u32x4 rw = make_rsrc(p.W, (unsigned)R * (K / 2));
+    const unsigned sz_bytes = ((unsigned)R * G * 2 + 3u) & ~3u;  // see the scale DMA below
+    const u32x4 rs = make_rsrc(p.wscale, sz_bytes);
+    const u32x4 rz = make_rsrc(p.wzero, sz_bytes);
+    int offx[CF::DX], offw[CF::DW];
+#pragma unroll
+    for (int i = 0; i < CF::DX; ++i) {
+        const int row = 4 * (wave * CF::DX + i) + (lane >> 4);
+        offx[i] = (c0 + row) * K * 2 + 16 * ((lane & 15) ^ (row & 7));
+    }
+#pragma unroll
+    for (int i = 0; i < CF::DW; ++i) {
+        const int row = 16 * (wave * CF::DW + i) + (lane >> 2);
+        offw[i] = (r0 + row) * (K / 2) + 16 * ((lane & 3) ^ ((row >> 1) & 3));
+    }
+    // scale / zero: instruction j (of 2 BR / 64) covers rows 64 (j % (BR/64)) + lane,
+    // scale for j < BR/64, zero otherwise.  Each lane fetches the aligned dword that
+    // holds its fp16; the byte range is rounded up to a dword, a read that stays
+    // inside the dword (and so the page) of the array's last element.
+    int srow[CF::DS];
+#pragma unroll
+    for (int i = 0; i < CF::DS; ++i) {
+        const int j = wave * CF::DS + i;
+        srow[i] = min(r0 + 64 * (j % (BR / 64)) + lane, R - 1);
+    }
+    u32x4 rxs = {0u, 0u, 0u, 0u};
+    if constexpr (XS) rxs = make_rsrc(p.xs, (unsigned)G * p.ldxs * 4);
+
+    auto issue = [&](int t) {
+        const int g = gbeg + t;
+        const unsigned st = lds0 + (unsigned)((t % S) * SB);
+#pragma unroll
+        for (int i = 0; i < CF::DX; ++i) dma16(rx, st + (wave * CF::DX + i) * 1024, offx[i], g * 256);
+#pragma unroll
+        for (int i = 0; i < CF::DW; ++i) dma16(rw, st + OFF_W + (wave * CF::DW + i) * 1024, offw[i], g * 64);
+#pragma unroll
+        for (int i = 0; i < CF::DS; ++i) {
+            const int j = wave * CF::DS + i;
+            const bool is_zero = j >= BR / 64;
+            const int voff = ((srow[i] * G + g) * 2) & ~3;
+            const unsigned dst = st + (is_zero ? OFF_ZR : OFF_SC) + (j % (BR / 64)) * 256;
+            dma4(is_zero ? rz : rs, dst, voff, 0);
+        }
+        if constexpr (XS) dma4(rxs, st + OFF_XS + wave * 256, (c0 + 64 * wave + lane) * 4, g * p.ldxs * 4);
+    };
+
+    // ---- fragment addressing ----
+    const int h = lane >> 5, l32 = lane & 31;
+    unsigned xoff[FX][8];  // X fragment of tile j, k-step s (relative to the stage)
+#pragma unroll
+    for (int j = 0; j < FX; ++j) {
+        const int xr = wc * 32 * FX + 32 * j + l32;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) xoff[j][s] = xr * 256 + 16 * ((8 * h + s) ^ (xr & 7));
+    }
+    unsigned woff[FW][2], wrow_loc[FW];
+    int wrow[FW];
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+        const int rl = wr * 32 * FW + 32 * i + l32;
+        wrow_loc[i] = rl;
+        wrow[i] = min(r0 + rl, R - 1);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) woff[i][e] = OFF_W + rl * 64 + 16 * ((2 * h + e) ^ ((rl >> 1) & 3));
+    }
+
+    f32x16 acc[FW][FX];
+#pragma unroll
+    for (int i = 0; i < FW; ++i)
+#pragma unroll
+        for (int j = 0; j < FX; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    const f32x16 zero16 = {};
+
+    // ---- prologue: stages 0 .. S-2 in flight ----
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t)
+        if (t < nkt) issue(t);
+
+    for (int t = 0; t < nkt; ++t) {
+        // stage t landed (everything issued after it may stay in flight), then
+        // the barrier: all waves' DMAs of stage t are complete and every wave
+        // has finished reading stage t - 1, whose buffer the next issue reuses
+        const int ahead = min(S - 2, nkt - 1 - t);
+        if (ahead >= 2) wait_vm<vmcnt_imm(2 * D)>();
+        else if (ahead == 1) wait_vm<vmcnt_imm(D)>();
+        else wait_vm<vmcnt_imm(0)>();
+        dma::stage_barrier<0xc07f>();
+        if (t + S - 1 < nkt) issue(t + S - 1);
+
+        const unsigned st = lds0 + (unsigned)((t % S) * SB);
+        const int g = gbeg + t;
+        // per-lane group scale (x 2^9) and packed -z 2^-9 of the lane's weight rows
+        float wsc[FW];
+        f16x2 zz[FW];
+#pragma unroll
+        for (int i = 0; i < FW; ++i) {
+            const int par = (wrow[i] * G + g) & 1;
+            const unsigned sd = lds_read4(st + OFF_SC + wrow_loc[i] * 4);
+            const unsigned zd = lds_read4(st + OFF_ZR + wrow_loc[i] * 4);
+            const uint16_t sh = (uint16_t)(par ? (sd >> 16) : (sd & 0xffffu));
+            const uint16_t zh = (uint16_t)(par ? (zd >> 16) : (zd & 0xffffu));
+            wsc[i] = h2f(sh) * 512.0f;
+            const _Float16 nz = (_Float16)(-rintf(h2f(zh)) * (1.0f / 512.0f));
+            zz[i] = f16x2{nz, nz};
+        }
+        u32x4 wraw[FW][2];
+#pragma unroll
+        for (int i = 0; i < FW; ++i)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) wraw[i][e] = lds_read16(st + woff[i][e]);
+
+        f32x16 P[FW][FX];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            f16x8 xf[FX], wf[FW];
+#pragma unroll
+            for (int j = 0; j < FX; ++j) xf[j] = bitcast<f16x8>(lds_read16(st + xoff[j][s]));
+#pragma unroll
+            for (int i = 0; i < FW; ++i) {
+                const u32x4& q = wraw[i][s >> 2];
+                const unsigned w = (s & 3) == 0 ? q.x : (s & 3) == 1 ? q.y : (s & 3) == 2 ? q.z : q.w;
+                wf[i] = unpack8(w, zz[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[j], wf[i], s == 0 ? zero16 : P[i][j],
+                                                                     0, 0, 0);
+        }
+
+        // ---- fold the group ----
+        if constexpr (XS) {
+#pragma unroll
+            for (int j = 0; j < FX; ++j) {
+                float sx[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const u32x4 v = lds_read16(st + OFF_XS + (wc * 32 * FX + 32 * j + 8 * q + 4 * h) * 4);
+                    sx[4 * q] = bitcast<float>(v.x);
+                    sx[4 * q + 1] = bitcast<float>(v.y);
+                    sx[4 * q + 2] = bitcast<float>(v.z);
+                    sx[4 * q + 3] = bitcast<float>(v.w);
+                }
+#pragma unroll
+                for (int i = 0; i < FW; ++i)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(wsc[i] * sx[v], P[i][j][v], acc[i][j][v]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(wsc[i], P[i][j][v], acc[i][j][v]);
+        }
+    }
+
+    // ---- split-K: publish, the last arriver sums all partials in split order ----
+    if (p.nsplit > 1) {
+        constexpr int NC = FW * FX * 4;  // f32x4 chunks per thread
+        // this split's slab: [chunk][thread] x 16 bytes, every chunk a contiguous row
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            p.part + (size_t)(tile * p.nsplit + split) * NC * CF::NT * 4, (short)0, NC * CF::NT * 16,
+            0x00020000);
+#pragma unroll
+        for (int i = 0; i < FW; ++i)
+#pragma unroll
+            for (int j = 0; j < FX; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                     acc[i][j][4 * q + 3]};
+                    store16_coherent(rp, (((i * FX + j) * 4 + q) * CF::NT + tid) * 16, v);
+                }
+        // the stages are dead here (every DMA was waited for, every read returned)
+        if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
+            return;
+#pragma unroll
+        for (int i = 0; i < FW; ++i)
+#pragma unroll
+            for (int j = 0; j < FX; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+        for (int sp = 0; sp < p.nsplit; ++sp) {
+            const float* src = p.part + ((size_t)(tile * p.nsplit + sp) * NC * CF::NT + tid) * 4;
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[i][j][4 * q + e] +=
+                                load_coherent(src + (size_t)((i * FX + j) * 4 + q) * CF::NT * 4 + e);
+        }
+    }
+
+    // ---- epilogue ----
+#pragma unroll
+    for (int i = 0; i < FW; ++i) {
+        const int r = r0 + wrow_loc[i];
+        if (r >= R) continue;
+#pragma unroll
+        for (int j = 0; j < FX; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = c0 + wc * 32 * FX + 32 * j + 8 * q + 4 * h;  // 4 consecutive columns
+                if constexpr (OUT == 0) {
+                    uint16_t* dst = p.out + (int64_t)r * p.C + c;
+                    if (c + 3 < p.C && (p.C & 3) == 0) {
+                        *reinterpret_cast<u32x2*>(dst) =
+                            u32x2{pack2h(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                  pack2h(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c + e < p.C) dst[e] = f2h(acc[i][j][4 * q + e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (c + e < p.C) {
+                            uint16_t* dst = p.out + (int64_t)(c + e) * R + r;
+                            float v = p.alpha * acc[i][j][4 * q + e];
+                            if (p.beta != 0.0f) v = fmaf(p.beta, h2f(*dst), v);
+                            *dst = f2h(v);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// B of group-wise INT4 ([K, ldb] bytes, two columns per byte, even n high) ->
+// Xt [Npad, K] fp16 = qB - rint(zB[g, n]) (exact), rows n >= N zero, and
+// xs [G, Npad] fp32 = sB (0 for n >= N).  Thread (n pair j, 8-k block kb);
+// consecutive threads take consecutive k blocks of one row pair, so the
+// 16-byte row stores coalesce.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) i4w_prep_b(const uint8_t* __restrict__ B, int ldb,
+                                                  const uint16_t* __restrict__ sB,
+                                                  const uint16_t* __restrict__ zB, int N, int K, int G,
+                                                  int Npad, uint16_t* __restrict__ Xt,
+                                                  float* __restrict__ xs) {
+    const int kblocks = K / 8;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)kblocks * (Npad / 2)) return;
+    const int kb = (int)(idx % kblocks), j = (int)(idx / kblocks);
+    const int k0 = 8 * kb, g = k0 / 128;
+    const int n0 = 2 * j, n1 = 2 * j + 1;
+    const bool in0 = n0 < N, in1 = n1 < N;
+    unsigned by[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) by[e] = in0 ? B[(int64_t)(k0 + e) * ldb + j] : 0u;
+    const float z0 = in0 ? rintf(h2f(zB[(int64_t)g * N + n0])) : 0.0f;
+    const float z1 = in1 ? rintf(h2f(zB[(int64_t)g * N + n1])) : 0.0f;
+    unsigned w0[4], w1[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const float a0 = in0 ? (float)(by[2 * d] >> 4) - z0 : 0.0f;
+        const float b0 = in0 ? (float)(by[2 * d + 1] >> 4) - z0 : 0.0f;
+        const float a1 = in1 ? (float)(by[2 * d] & 15u) - z1 : 0.0f;
+        const float b1 = in1 ? (float)(by[2 * d + 1] & 15u) - z1 : 0.0f;
+        w0[d] = pack2h(a0, b0);
+        w1[d] = pack2h(a1, b1);
+    }
+    *reinterpret_cast<u32x4*>(Xt + (int64_t)n0 * K + k0) = u32x4{w0[0], w0[1], w0[2], w0[3]};
+    *reinterpret_cast<u32x4*>(Xt + (int64_t)n1 * K + k0) = u32x4{w1[0], w1[1], w1[2], w1[3]};
+    if ((kb & 15) == 0) {
+        xs[(int64_t)g * Npad + n0] = in0 ? h2f(sB[(int64_t)g * N + n0]) : 0.0f;
+        xs[(int64_t)g * Npad + n1] = in1 ? h2f(sB[(int64_t)g * N + n1]) : 0.0f;
+    }
+}
+
+}  // namespace i4w
+}  // namespace clove

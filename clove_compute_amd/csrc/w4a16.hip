@@ -296,6 +296,10 @@ clove_status_t launch_w4a16(const W4A16Args& a, hipStream_t stream) {
         if (tv == 2) return run_gemv<2>(p, aligned, dev.num_cus, stream);
         return run_gemv<4>(p, aligned, dev.num_cus, stream);
     }
+    if (a.K > 0) {
+        clove_status_t st2;
+        if (try_i4w_w4a16(a, dev.num_cus, stream, &st2)) return st2;
+    }
     mg::Params p{};
     p.a = a.X;
     p.b = a.W; p.b_scale = a.scale; p.b_zero = a.zero;

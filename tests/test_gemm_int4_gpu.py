@@ -122,3 +122,29 @@ def test_quantizer_round_trip_through_kernel():
         quant.pack_rows(quant.unpack_cols(B_q, N).T), sB.T, zB.T, K).T
     ok, rep = within_tol(C, ref)
     assert ok, rep
+
+
+# group-wise, N > 8, K % 128 == 0 takes the INT4-weight MFMA kernel (i4w_gemm)
+# after the B transpose: every tile configuration, ragged M and N (odd N: the
+# last byte column's low nibble is padding), split K
+@pytest.mark.parametrize("M,N,K", [(77, 17, 256), (300, 33, 1024), (129, 100, 512), (1000, 200, 1024),
+                                   (8192, 1024, 256), (4096, 9, 11008)])
+def test_groupwise_mfma_path(M, N, K):
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "mfma")
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    g = rng("rows-mfma", M, N, K)
+    rows = np.arange(M) if M <= 1000 else np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 32)]))
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
+    ok, rep = within_tol(C[rows], ref)
+    assert ok, rep
+    assert np.all(np.isfinite(C.astype(np.float32)))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 16, 11008), (1000, 200, 1024), (8192, 1024, 256)])
+def test_groupwise_mfma_path_pow2_bit_exact(M, N, K):
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2m", pow2=True, small=True)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    g = rng("rows-p2", M, N, K)
+    rows = np.arange(M) if M <= 1000 else np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 32)]))
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
+    assert np.array_equal(f16bits(C[rows]), f16bits(ref.astype(np.float16)))

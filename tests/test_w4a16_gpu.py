@@ -77,3 +77,26 @@ def test_ragged(T, O, K):
     _, ref = oracle.w4a16(X, W, s, z, Yin, 0.5, 1.0)
     ok, rep = within_tol(Y, ref)
     assert ok, rep
+
+
+# K % 128 == 0 and T > 4 take the INT4-weight MFMA kernel (i4w_gemm): every
+# tile configuration (X rows <= 32, <= 64, 128 x 128, 256 x 128), ragged
+# token and weight-row counts, split K, alpha/beta
+@pytest.mark.parametrize("T,O,K", [(6, 1000, 4096), (37, 300, 1024), (100, 200, 2048), (257, 129, 384),
+                                   (1024, 8192, 256), (512, 3072, 2048)])
+def test_mfma_path_shapes(T, O, K):
+    X, W, s, z, g = make(T, O, K, "mfma")
+    Yin = g.standard_normal((T, O)).astype(np.float16)
+    Y = run(X, W, s, z, Yin, O, 0.5, 1.0)
+    rows = np.arange(T) if T <= 300 else np.unique(np.concatenate([[0, T - 1], g.integers(0, T, 24)]))
+    _, ref = oracle.w4a16(X[rows], W, s, z, Yin[rows], 0.5, 1.0)
+    ok, rep = within_tol(Y[rows], ref)
+    assert ok, rep
+
+
+@pytest.mark.parametrize("T,O,K", [(6, 1000, 4096), (200, 640, 1024), (1024, 8192, 256)])
+def test_mfma_path_pow2_bit_exact(T, O, K):
+    X, W, s, z, _ = make(T, O, K, "pow2m", pow2=True)
+    Y = run(X, W, s, z, None, O)
+    _, ref = oracle.w4a16(X, W, s, z)
+    assert np.array_equal(f16bits(Y), f16bits(ref.astype(np.float16)))
