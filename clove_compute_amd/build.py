@@ -34,6 +34,12 @@ CFLAGS = [
 ]
 
 
+# per-source additions: the INT4-weight GEMM keeps its per-group MFMA sums in
+# VGPRs (the group fold reads every one of them; in AGPRs each read would be a
+# separate v_accvgpr_read)
+EXTRA = {"i4w_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
@@ -48,7 +54,7 @@ def _compile(src: str, force: bool) -> str:
     if (not force and os.path.exists(obj)
             and os.path.getmtime(obj) >= max(os.path.getmtime(src), _headers_mtime())):
         return obj
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj + ".tmp"]
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj + ".tmp"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -98,5 +98,60 @@ __device__ __forceinline__ bool splitk_arrive_is_last(unsigned* counter, unsigne
     return *lds_flag != 0;
 }
 
+// ---------------------------------------------------------------------------
+// Split-K partial tiles, 16 bytes per access.  A split's slab holds NC chunks
+// of 16 bytes per thread, laid out [chunk][thread] so that every chunk is one
+// contiguous row of NT x 16 bytes.  Stores and loads carry cache policy sc1
+// (device-coherent: written through past the XCD-private L2, read from the
+// coherent level) and go through compiler builtins, never inline asm: the
+// backend must see a store to keep its data registers intact until the
+// hardware has read them.  The sum runs in split order (deterministic).
+// ---------------------------------------------------------------------------
+constexpr int kCpolSc1 = 16;
+
+template <int NC, int NT>
+__device__ __forceinline__ void splitk_publish(float* slab, int tid, const f32x4 (&v)[NC]) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(slab, (short)0, NC * NT * 16, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        __builtin_amdgcn_raw_buffer_store_b128(bitcast<u32x4>(v[c]), r, (c * NT + tid) * 16, 0, kCpolSc1);
+}
+
+// slabs: the nsplit consecutive slabs of one tile; INT sums int32 lanes.
+// Chunks are reduced 16 at a time (bounded registers); within a group, two
+// splits' loads are in flight at once.
+template <int NC, int NT, bool INT>
+__device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, int tid, f32x4 (&sum)[NC]) {
+    constexpr int CG = NC < 16 ? NC : 16;
+    static_assert(NC % CG == 0, "chunk groups");
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(slabs), (short)0, nsplit * NC * NT * 16, 0x00020000);
+    auto load = [&](int sp, int c0, f32x4* v) {
+#pragma unroll
+        for (int c = 0; c < CG; ++c)
+            v[c] = bitcast<f32x4>(
+                __builtin_amdgcn_raw_buffer_load_b128(r, ((sp * NC + c0 + c) * NT + tid) * 16, 0, kCpolSc1));
+    };
+    auto add = [](f32x4& a, const f32x4& b) {
+        if constexpr (INT) a = bitcast<f32x4>(bitcast<i32x4>(a) + bitcast<i32x4>(b));
+        else a += b;
+    };
+#pragma unroll
+    for (int c0 = 0; c0 < NC; c0 += CG) {
+        load(0, c0, sum + c0);
+        for (int sp = 1; sp < nsplit; sp += 2) {
+            f32x4 a[CG], b[CG];
+            const bool two = sp + 1 < nsplit;
+            load(sp, c0, a);
+            load(two ? sp + 1 : sp, c0, b);
+#pragma unroll
+            for (int c = 0; c < CG; ++c) {
+                add(sum[c0 + c], a[c]);
+                if (two) add(sum[c0 + c], b[c]);
+            }
+        }
+    }
+}
+
 }  // namespace hw
 }  // namespace clove

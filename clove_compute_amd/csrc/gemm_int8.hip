@@ -242,33 +242,31 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
     }
 
     if (p.nsplit > 1) {
+        constexpr int NC = FN * FM * 4;  // 16-byte chunks of int32 partials per thread
         const int tile_id = tc.tm * p.tiles_n + tc.tn;
-        float* ws_tile = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
-        float* mine = ws_tile + (int64_t)tc.split * (BM * BN);
+        float* slabs = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
+        f32x4 v[NC];
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int j = 0; j < FM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    store_coherent(&mine[((i * FM + j) * 16 + r) * NT + tid], __int_as_float(acc[i][j][r]));
+                for (int q = 0; q < 4; ++q)
+                    v[(i * FM + j) * 4 + q] = bitcast<f32x4>(i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                                   acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+        splitk_publish<NC, NT>(slabs + (int64_t)tc.split * (BM * BN), tid, v);
         if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
+        splitk_reduce<NC, NT, true>(slabs, p.nsplit, tid, v);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int j = 0; j < FM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-        for (int s = 0; s < p.nsplit; ++s) {
-            const float* part = ws_tile + (int64_t)s * (BM * BN);
+                for (int q = 0; q < 4; ++q) {
+                    const i32x4 w = bitcast<i32x4>(v[(i * FM + j) * 4 + q]);
 #pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-                for (int j = 0; j < FM; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc[i][j][r] += __float_as_int(load_coherent(&part[((i * FM + j) * 16 + r) * NT + tid]));
-        }
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = w[e];
+                }
     }
 
 #pragma unroll

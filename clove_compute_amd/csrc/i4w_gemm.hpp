@@ -109,16 +109,6 @@ __device__ __forceinline__ void dma4(const u32x4& rsrc, unsigned lds_addr, int v
                  : "memory");
 }
 
-// 16-byte store that is visible device-wide once complete (cache policy sc1:
-// written through past the XCD-private L2), for split-K partials.  A compiler
-// builtin rather than inline asm: the backend must see the store to keep its
-// data registers live until the hardware has read them (a VALU write right
-// after a >8-byte store would otherwise race with it).
-constexpr int kCpolSc1 = 16;
-__device__ __forceinline__ void store16_coherent(__amdgpu_buffer_rsrc_t rsrc, int byte_off, const f32x4& v) {
-    __builtin_amdgcn_raw_buffer_store_b128(bitcast<u32x4>(v), rsrc, byte_off, 0, kCpolSc1);
-}
-
 // (q - z) * 2^-9 for the 8 nibbles of one dword, in k order; zz = -z * 2^-9
 __device__ __forceinline__ f16x8 unpack8(unsigned w, f16x2 zz) {
     const unsigned hr = w & 0xf0f0f0f0u, lo = w & 0x0f0f0f0fu;
@@ -200,9 +190,9 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     u32x4 rxs = {0u, 0u, 0u, 0u};
     if constexpr (XS) rxs = make_rsrc(p.xs, (unsigned)G * p.ldxs * 4);
 
-    auto issue = [&](int t) {
+    auto issue = [&](int t, int stage) {
         const int g = gbeg + t;
-        const unsigned st = lds0 + (unsigned)((t % S) * SB);
+        const unsigned st = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(stage * SB));
 #pragma unroll
         for (int i = 0; i < CF::DX; ++i) dma16(rx, st + (wave * CF::DX + i) * 1024, offx[i], g * 256);
 #pragma unroll
@@ -218,25 +208,23 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         if constexpr (XS) dma4(rxs, st + OFF_XS + wave * 256, (c0 + 64 * wave + lane) * 4, g * p.ldxs * 4);
     };
 
-    // ---- fragment addressing ----
+    // ---- fragment addressing.  Rows of a lane differ between tiles by a
+    // multiple of 32, which leaves the swizzle (low row bits) unchanged, so
+    // per k-step one per-lane offset serves every tile and the tile enters as
+    // an immediate: X row x, step s at 256 x + 16 ((8 h + s) ^ (x & 7)), with
+    // (8 h + s) ^ (x & 7) = 8 h + (s ^ (lane & 7)); weight row r, half e at
+    // 64 r + 16 ((2 h + e) ^ ((lane >> 1) & 3)).
     const int h = lane >> 5, l32 = lane & 31;
-    unsigned xoff[FX][8];  // X fragment of tile j, k-step s (relative to the stage)
+    const int xrow0 = wc * 32 * FX + l32, wrow0 = wr * 32 * FW + l32;
+    unsigned xoff[8];
 #pragma unroll
-    for (int j = 0; j < FX; ++j) {
-        const int xr = wc * 32 * FX + 32 * j + l32;
+    for (int s = 0; s < 8; ++s) xoff[s] = xrow0 * 256 + 16 * (8 * h + (s ^ (lane & 7)));
+    unsigned woff[2];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) xoff[j][s] = xr * 256 + 16 * ((8 * h + s) ^ (xr & 7));
-    }
-    unsigned woff[FW][2], wrow_loc[FW];
+    for (int e = 0; e < 2; ++e) woff[e] = OFF_W + wrow0 * 64 + 16 * ((2 * h + e) ^ ((lane >> 1) & 3));
     int wrow[FW];
 #pragma unroll
-    for (int i = 0; i < FW; ++i) {
-        const int rl = wr * 32 * FW + 32 * i + l32;
-        wrow_loc[i] = rl;
-        wrow[i] = min(r0 + rl, R - 1);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) woff[i][e] = OFF_W + rl * 64 + 16 * ((2 * h + e) ^ ((rl >> 1) & 3));
-    }
+    for (int i = 0; i < FW; ++i) wrow[i] = min(r0 + wrow0 + 32 * i, R - 1);
 
     f32x16 acc[FW][FX];
 #pragma unroll
@@ -250,8 +238,11 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     // ---- prologue: stages 0 .. S-2 in flight ----
 #pragma unroll
     for (int t = 0; t < S - 1; ++t)
-        if (t < nkt) issue(t);
+        if (t < nkt) issue(t, t);
 
+    // stage of tile t (t % S) and of tile t + S - 1 ((t - 1) % S), kept as
+    // uniform counters
+    int stage = 0, stage_next = S - 1;
     for (int t = 0; t < nkt; ++t) {
         // stage t landed (everything issued after it may stay in flight), then
         // the barrier: all waves' DMAs of stage t are complete and every wave
@@ -261,18 +252,21 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         else if (ahead == 1) wait_vm<vmcnt_imm(D)>();
         else wait_vm<vmcnt_imm(0)>();
         dma::stage_barrier<0xc07f>();
-        if (t + S - 1 < nkt) issue(t + S - 1);
+        if (t + S - 1 < nkt) issue(t + S - 1, stage_next);
 
-        const unsigned st = lds0 + (unsigned)((t % S) * SB);
+        const unsigned st = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(stage * SB));
+        stage_next = stage;
+        stage = stage + 1 == S ? 0 : stage + 1;
         const int g = gbeg + t;
         // per-lane group scale (x 2^9) and packed -z 2^-9 of the lane's weight rows
         float wsc[FW];
         f16x2 zz[FW];
+        const unsigned sbase = st + OFF_SC + wrow0 * 4;
 #pragma unroll
         for (int i = 0; i < FW; ++i) {
             const int par = (wrow[i] * G + g) & 1;
-            const unsigned sd = lds_read4(st + OFF_SC + wrow_loc[i] * 4);
-            const unsigned zd = lds_read4(st + OFF_ZR + wrow_loc[i] * 4);
+            const unsigned sd = lds_read4(sbase + 128 * i);
+            const unsigned zd = lds_read4(sbase + (OFF_ZR - OFF_SC) + 128 * i);
             const uint16_t sh = (uint16_t)(par ? (sd >> 16) : (sd & 0xffffu));
             const uint16_t zh = (uint16_t)(par ? (zd >> 16) : (zd & 0xffffu));
             wsc[i] = h2f(sh) * 512.0f;
@@ -281,16 +275,19 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         }
         u32x4 wraw[FW][2];
 #pragma unroll
-        for (int i = 0; i < FW; ++i)
+        for (int e = 0; e < 2; ++e) {
+            const unsigned wb = st + woff[e];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) wraw[i][e] = lds_read16(st + woff[i][e]);
+            for (int i = 0; i < FW; ++i) wraw[i][e] = lds_read16(wb + 2048 * i);
+        }
 
         f32x16 P[FW][FX];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             f16x8 xf[FX], wf[FW];
+            const unsigned xb = st + xoff[s];
 #pragma unroll
-            for (int j = 0; j < FX; ++j) xf[j] = bitcast<f16x8>(lds_read16(st + xoff[j][s]));
+            for (int j = 0; j < FX; ++j) xf[j] = bitcast<f16x8>(lds_read16(xb + 8192 * j));
 #pragma unroll
             for (int i = 0; i < FW; ++i) {
                 const u32x4& q = wraw[i][s >> 2];
@@ -312,7 +309,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
                 float sx[16];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const u32x4 v = lds_read16(st + OFF_XS + (wc * 32 * FX + 32 * j + 8 * q + 4 * h) * 4);
+                    const u32x4 v = lds_read16(st + OFF_XS + (wc * 32 * FX + 4 * h) * 4 + (32 * j + 8 * q) * 4);
                     sx[4 * q] = bitcast<float>(v.x);
                     sx[4 * q + 1] = bitcast<float>(v.y);
                     sx[4 * q + 2] = bitcast<float>(v.z);
@@ -336,48 +333,35 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     // ---- split-K: publish, the last arriver sums all partials in split order ----
     if (p.nsplit > 1) {
         constexpr int NC = FW * FX * 4;  // f32x4 chunks per thread
-        // this split's slab: [chunk][thread] x 16 bytes, every chunk a contiguous row
-        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-            p.part + (size_t)(tile * p.nsplit + split) * NC * CF::NT * 4, (short)0, NC * CF::NT * 16,
-            0x00020000);
+        f32x4 v[NC];
 #pragma unroll
         for (int i = 0; i < FW; ++i)
 #pragma unroll
             for (int j = 0; j < FX; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
-                                     acc[i][j][4 * q + 3]};
-                    store16_coherent(rp, (((i * FX + j) * 4 + q) * CF::NT + tid) * 16, v);
-                }
+                for (int q = 0; q < 4; ++q)
+                    v[(i * FX + j) * 4 + q] = f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                    acc[i][j][4 * q + 3]};
+        float* slabs = p.part + (size_t)tile * p.nsplit * NC * CF::NT * 4;
+        splitk_publish<NC, CF::NT>(slabs + (size_t)split * NC * CF::NT * 4, tid, v);
         // the stages are dead here (every DMA was waited for, every read returned)
         if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
             return;
+        splitk_reduce<NC, CF::NT, false>(slabs, p.nsplit, tid, v);
 #pragma unroll
         for (int i = 0; i < FW; ++i)
 #pragma unroll
             for (int j = 0; j < FX; ++j)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-        for (int sp = 0; sp < p.nsplit; ++sp) {
-            const float* src = p.part + ((size_t)(tile * p.nsplit + sp) * NC * CF::NT + tid) * 4;
+                for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int i = 0; i < FW; ++i)
-#pragma unroll
-                for (int j = 0; j < FX; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[i][j][4 * q + e] +=
-                                load_coherent(src + (size_t)((i * FX + j) * 4 + q) * CF::NT * 4 + e);
-        }
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = v[(i * FX + j) * 4 + q][e];
     }
 
     // ---- epilogue ----
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
-        const int r = r0 + wrow_loc[i];
+        const int r = r0 + wrow0 + 32 * i;
         if (r >= R) continue;
 #pragma unroll
         for (int j = 0; j < FX; ++j) {

@@ -613,33 +613,29 @@ __global__ void __launch_bounds__(T::NT) mfma_gemm(Params p) {
     }
 
     if (SPLITK && p.nsplit > 1) {
+        constexpr int NC = FN * FM * 4;  // f32x4 chunks per thread
         const int tile_id = (tc.batch * p.tiles_m + tc.tm) * p.tiles_n + tc.tn;
-        float* ws_tile = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
-        float* mine = ws_tile + (int64_t)tc.split * (BM * BN);
+        float* slabs = p.ws + (int64_t)tile_id * p.nsplit * (BM * BN);
+        f32x4 v[NC];
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int j = 0; j < FM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    store_coherent(&mine[((i * FM + j) * 16 + r) * NT + tid], acc[i][j][r]);
+                for (int q = 0; q < 4; ++q)
+                    v[(i * FM + j) * 4 + q] = f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                    acc[i][j][4 * q + 3]};
+        splitk_publish<NC, NT>(slabs + (int64_t)tc.split * (BM * BN), tid, v);
         if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
+        splitk_reduce<NC, NT, false>(slabs, p.nsplit, tid, v);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int j = 0; j < FM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-        for (int s = 0; s < p.nsplit; ++s) {
-            const float* part = ws_tile + (int64_t)s * (BM * BN);
+                for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-                for (int j = 0; j < FM; ++j)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        acc[i][j][r] += load_coherent(&part[((i * FM + j) * 16 + r) * NT + tid]);
-        }
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = v[(i * FM + j) * 4 + q][e];
     }
 
     uint16_t* C = p.c + tc.batch * p.strideC;
