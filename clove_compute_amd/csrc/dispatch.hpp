@@ -84,6 +84,13 @@ clove_status_t launch_w4a16(const W4A16Args& args, hipStream_t stream);
 bool try_i4w_w4a16(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 bool try_i4w_int4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 
+// MFMA path for few rows of A against a large N-contiguous B (skinny_gemm.hip):
+// FP16 (any alpha/beta, batched) and INT8 with zero points 0.  Same contract
+// as the try_i4w_* functions.
+bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N, int K,
+                     float alpha, float beta, int num_cus, hipStream_t stream, clove_status_t* status);
+bool try_skinny_int8(const Int8Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+
 inline clove_status_t check_launch() {
     return hipGetLastError() == hipSuccess ? CLOVE_OK : CLOVE_ERR_LAUNCH;
 }

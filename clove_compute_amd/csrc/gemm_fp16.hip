@@ -281,6 +281,10 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
     const int64_t big_tiles = (int64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
     if (big_tiles >= cus / 2 && dma_eligible(A, B, C, M, N, K))
         return run_dma(A, B, C, batch, M, N, K, alpha, beta, stream);
+    {
+        clove_status_t st2;
+        if (try_skinny_fp16(A, B, C, batch, M, N, K, alpha, beta, cus, stream, &st2)) return st2;
+    }
     if (aligned) {
         if (big_tiles >= cus / 2) return run_mfma<Tile<256, 256, 64, 2, 2>, true>(p, batch, cus, stream);
         if (M <= 32) return run_mfma<Tile<32, 128, 64, 1, 4>, true>(p, batch, cus, stream);

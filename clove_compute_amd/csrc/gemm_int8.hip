@@ -488,6 +488,10 @@ clove_status_t launch_gemm_int8(const Int8Args& a, hipStream_t stream) {
     p.scale = a.scale; p.za = a.za; p.zb = a.zb;
     p.M = a.M; p.N = a.N; p.K = a.K;
     const bool aligned = aligned16(a.A) && aligned16(a.B) && (a.K % 16 == 0) && (a.N % 16 == 0);
+    if (a.M > 4) {
+        clove_status_t st2;
+        if (try_skinny_int8(a, dev.num_cus, stream, &st2)) return st2;
+    }
     switch (a.out) {
         case Int8Out::kHalfPerTensor: return dispatch<(int)Int8Out::kHalfPerTensor>(p, aligned, dev.num_cus, stream);
         case Int8Out::kHalfRowCol: return dispatch<(int)Int8Out::kHalfRowCol>(p, aligned, dev.num_cus, stream);

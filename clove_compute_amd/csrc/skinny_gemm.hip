@@ -1,0 +1,108 @@
+// Host side of the skinny GEMM (skinny_gemm.hpp): tile configuration by M,
+// split-K plan, scratch.
+#include "dispatch.hpp"
+#include "skinny_gemm.hpp"
+
+namespace clove {
+namespace {
+
+using namespace sk;
+
+// (I8, BM, BN, WM, WN, stages)
+using F16M32 = Cfg<false, 32, 128, 1, 4, 5>;
+using F16M64 = Cfg<false, 64, 128, 2, 2, 4>;
+using F16M128 = Cfg<false, 128, 64, 4, 1, 4>;
+using I8M32 = Cfg<true, 32, 128, 1, 4, 5>;
+using I8M64 = Cfg<true, 64, 128, 2, 2, 4>;
+using I8M128 = Cfg<true, 128, 64, 4, 1, 4>;
+
+template <class CF, int OUT>
+clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
+    a.tiles_m = cdiv(a.M, CF::BM);
+    a.tiles_n = cdiv(a.N, CF::BN);
+    const int tiles = a.tiles_m * a.tiles_n * batch;
+    const int nk = a.K / CF::BK;
+    // split K (whole K tiles, at least two per split) until about one
+    // workgroup per CU
+    int ns = tiles >= cus ? 1 : cus / tiles;
+    ns = max(1, min(ns, nk / 2));
+    const int kt_per = cdiv(nk, ns);
+    a.kps = kt_per * CF::BK;
+    a.nsplit = cdiv(nk, kt_per);
+    if (a.nsplit > 1) {
+        Scratch s;
+        const size_t bytes = (size_t)tiles * a.nsplit * CF::NT * CF::FM * CF::FN * 16 * sizeof(float);
+        const clove_status_t st = acquire_scratch(stream, bytes, (size_t)tiles, &s);
+        if (st != CLOVE_OK) return st;
+        a.part = s.partials;
+        a.counters = s.counters;
+    }
+    auto k = skinny_gemm<CF, OUT>;
+    if (CF::LDS > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            CF::LDS) != hipSuccess)
+        return CLOVE_ERR_LAUNCH;
+    hipLaunchKernelGGL(k, dim3((unsigned)(tiles * a.nsplit)), dim3(CF::NT), CF::LDS, stream, a);
+    return check_launch();
+}
+
+bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
+
+}  // namespace
+
+bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N, int K,
+                     float alpha, float beta, int cus, hipStream_t stream, clove_status_t* status) {
+    if (M <= 4 || M > 512 || K <= 0 || K % 64 != 0 || N < 8 || N % 8 != 0) return false;
+    if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return false;
+    // (the DMA offsets of the padded rows m < M + 128 must stay 32-bit)
+    if (!fits31((int64_t)(M + 128) * K * 2) || !fits31((int64_t)K * N * 2) || !fits31((int64_t)M * N * 2))
+        return false;
+    Args a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.sA = (int64_t)M * K;
+    a.sB = (int64_t)K * N;
+    a.sC = (int64_t)M * N;
+    if (M <= 32) *status = run<F16M32, kF16AlphaBeta>(a, batch, cus, stream);
+    else if (M <= 64) *status = run<F16M64, kF16AlphaBeta>(a, batch, cus, stream);
+    else *status = run<F16M128, kF16AlphaBeta>(a, batch, cus, stream);
+    return true;
+}
+
+bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_status_t* status) {
+    if (q.M <= 4 || q.M > 512 || q.K <= 0 || q.K % 128 != 0 || q.N < 16 || q.N % 16 != 0) return false;
+    if (q.za != 0 || q.zb != 0 || !aligned16(q.A) || !aligned16(q.B) || !aligned16(q.C)) return false;
+    if (!fits31((int64_t)(q.M + 128) * q.K) || !fits31((int64_t)q.K * q.N) || !fits31((int64_t)q.M * q.N * 4))
+        return false;
+    Args a{};
+    a.A = q.A;
+    a.B = q.B;
+    a.C = q.C;
+    a.sa = q.sa;
+    a.sb = q.sb;
+    a.scale = q.scale;
+    a.M = q.M;
+    a.N = q.N;
+    a.K = q.K;
+    auto pick = [&](auto out_tag) -> clove_status_t {
+        constexpr int OUT = decltype(out_tag)::value;
+        if (q.M <= 32) return run<I8M32, OUT>(a, 1, cus, stream);
+        if (q.M <= 64) return run<I8M64, OUT>(a, 1, cus, stream);
+        return run<I8M128, OUT>(a, 1, cus, stream);
+    };
+    switch (q.out) {
+        case Int8Out::kHalfPerTensor: *status = pick(std::integral_constant<int, kI8Tensor>{}); break;
+        case Int8Out::kHalfRowCol: *status = pick(std::integral_constant<int, kI8RowCol>{}); break;
+        case Int8Out::kAcc32: *status = pick(std::integral_constant<int, kI8Acc32>{}); break;
+        default: return false;
+    }
+    return true;
+}
+
+}  // namespace clove

@@ -226,3 +226,30 @@ def test_big_shape_k_not_multiple_of_tile():
     C = run_fp16(A, B)
     rows = np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 16)]))
     check_rows(A, B, C, rows)
+
+
+# 4 < M <= 512 with K % 64 == 0, N % 8 == 0 and 16-byte aligned operands take
+# the skinny kernel (B through LDS DMA and transposing LDS reads): every
+# M configuration (<= 32, <= 64, <= 512), ragged M and N, split K, alpha/beta
+@pytest.mark.parametrize("M,N,K", [(5, 4096, 4096), (17, 136, 192), (33, 520, 1024), (64, 4096, 2048),
+                                   (65, 72, 64), (129, 1000, 4096), (250, 4096, 512), (512, 8, 128)])
+def test_skinny_shapes(M, N, K):
+    g = rng("skinny", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.02).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=0.75, beta=-0.5)
+    rows = np.arange(M) if M <= 64 else np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 24)]))
+    check_rows(A, B, C, rows, C0, 0.75, -0.5)
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 4096, 4096), (100, 264, 640), (128, 4096, 4096)])
+def test_skinny_small_integers_bit_exact(M, N, K):
+    # |a|, |b| <= 4 integers: every product and partial sum is exact in fp32,
+    # so split K and the fp16 output are exact
+    g = rng("skinny-int", M, N, K)
+    A = g.integers(-4, 5, (M, K)).astype(np.float16)
+    B = g.integers(-4, 5, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    ref = oracle.gemm_fp16_f64(A, B).astype(np.float16)
+    assert np.array_equal(f16bits(C), f16bits(ref))

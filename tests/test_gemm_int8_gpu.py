@@ -101,3 +101,25 @@ def test_broadcast_rowcol_equals_per_tensor():
                            M, N, K, 2, -3)
     _sync()
     assert np.array_equal(f16bits(to_host(C1)), f16bits(to_host(C2)))
+
+
+# 4 < M <= 512, zero points 0, K % 128 == 0, N % 16 == 0: the skinny kernel
+# (int8 B through LDS DMA and ds_read_b64_tr_b8); int32 partials keep split K exact
+@pytest.mark.parametrize("M,N,K", [(5, 4096, 4096), (31, 272, 384), (64, 1024, 4096), (100, 48, 128),
+                                   (128, 4096, 1024), (300, 512, 2048)])
+def test_skinny_bit_exact(M, N, K):
+    g = rng("skinny8", M, N, K)
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    sa = g.uniform(0.001, 0.02, M).astype(np.float16)
+    sb = g.uniform(0.001, 0.02, N).astype(np.float16)
+    s1, s2 = np.float32(g.uniform(0.001, 0.05)), np.float32(g.uniform(0.001, 0.05))
+    C1, C2 = empty_f16(M, N), empty_f16(M, N)
+    _cg().gemm_int8(to_dev(A), to_dev(B), C1, M, N, K, float(s1), 0, float(s2), 0)
+    _cg().gemm_int8_rowcol(to_dev(A), to_dev(B), to_dev(sa), to_dev(sb), C2, M, N, K)
+    _sync()
+    Cref1, accref = oracle.gemm_int8(A, B, s1, 0, s2, 0)
+    Cref2, _ = oracle.gemm_int8_rowcol(A, B, sa, sb)
+    assert np.array_equal(run_acc32(A, B), accref)
+    assert np.array_equal(f16bits(to_host(C1)), f16bits(Cref1))
+    assert np.array_equal(f16bits(to_host(C2)), f16bits(Cref2))
