@@ -118,36 +118,38 @@ __device__ __forceinline__ void splitk_publish(float* slab, int tid, const f32x4
 }
 
 // slabs: the nsplit consecutive slabs of one tile; INT sums int32 lanes.
-// Chunks are reduced 16 at a time (bounded registers); within a group, two
-// splits' loads are in flight at once.
+// Chunks are reduced 16 at a time (bounded registers); within a chunk group
+// the loads of SB splits (up to 32 loads) are in flight together, so a small
+// tile needs one round trip to the coherent level for all of its splits.
 template <int NC, int NT, bool INT>
 __device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, int tid, f32x4 (&sum)[NC]) {
     constexpr int CG = NC < 16 ? NC : 16;
+    constexpr int SB = 32 / CG > 1 ? 32 / CG : 1;
     static_assert(NC % CG == 0, "chunk groups");
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(slabs), (short)0, nsplit * NC * NT * 16, 0x00020000);
-    auto load = [&](int sp, int c0, f32x4* v) {
-#pragma unroll
-        for (int c = 0; c < CG; ++c)
-            v[c] = bitcast<f32x4>(
-                __builtin_amdgcn_raw_buffer_load_b128(r, ((sp * NC + c0 + c) * NT + tid) * 16, 0, kCpolSc1));
-    };
-    auto add = [](f32x4& a, const f32x4& b) {
-        if constexpr (INT) a = bitcast<f32x4>(bitcast<i32x4>(a) + bitcast<i32x4>(b));
-        else a += b;
-    };
 #pragma unroll
     for (int c0 = 0; c0 < NC; c0 += CG) {
-        load(0, c0, sum + c0);
-        for (int sp = 1; sp < nsplit; sp += 2) {
-            f32x4 a[CG], b[CG];
-            const bool two = sp + 1 < nsplit;
-            load(sp, c0, a);
-            load(two ? sp + 1 : sp, c0, b);
+        for (int s0 = 0; s0 < nsplit; s0 += SB) {
+            f32x4 buf[SB][CG];
 #pragma unroll
-            for (int c = 0; c < CG; ++c) {
-                add(sum[c0 + c], a[c]);
-                if (two) add(sum[c0 + c], b[c]);
+            for (int b = 0; b < SB; ++b) {
+                const int sp = min(s0 + b, nsplit - 1);  // past the end: a harmless repeat
+#pragma unroll
+                for (int c = 0; c < CG; ++c)
+                    buf[b][c] = bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(
+                        r, ((sp * NC + c0 + c) * NT + tid) * 16, 0, kCpolSc1));
+            }
+#pragma unroll
+            for (int b = 0; b < SB; ++b) {
+                if (s0 + b >= nsplit) break;
+#pragma unroll
+                for (int c = 0; c < CG; ++c) {
+                    if (s0 + b == 0) sum[c0 + c] = buf[b][c];
+                    else if constexpr (INT)
+                        sum[c0 + c] = bitcast<f32x4>(bitcast<i32x4>(sum[c0 + c]) + bitcast<i32x4>(buf[b][c]));
+                    else sum[c0 + c] += buf[b][c];
+                }
             }
         }
     }

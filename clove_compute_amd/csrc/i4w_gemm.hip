@@ -12,7 +12,7 @@ using namespace i4w;
 // tiles per wave in each direction
 using CfgBig = Cfg<4, 1, 2, 4, 3>;  // 256 x 128, 4 waves of 64 x 128
 using CfgSq = Cfg<2, 2, 2, 2, 3>;   // 128 x 128, 4 waves of 64 x 64
-using CfgC64 = Cfg<4, 1, 1, 2, 3>;  // 128 x 64
+using CfgC64 = Cfg<4, 1, 1, 2, 3>;  // 128 x 64 (75 KB LDS: two workgroups per CU)
 using CfgC32 = Cfg<2, 1, 1, 1, 4>;  // 64 x 32, 2 waves (several workgroups per CU)
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -21,15 +21,17 @@ struct Plan {
     int tiles_r, tiles_c, nsplit, gps;
 };
 
-// split K (whole groups, at least two per split) until the grid reaches `target`
+// No split when the tiles cover 3/4 of the CUs; otherwise split K (whole
+// groups, at least min_groups per split) until the grid reaches `target`
+// workgroups (the number that can be resident at once).
 template <class CF>
-Plan make_plan(int R, int C, int G, int target) {
+Plan make_plan(int R, int C, int G, int cus, int target, int min_groups) {
     Plan pl;
     pl.tiles_r = cdiv(R, CF::BR);
     pl.tiles_c = cdiv(C, CF::BC);
     const int tiles = pl.tiles_r * pl.tiles_c;
-    int ns = tiles >= target ? 1 : target / tiles;
-    ns = max(1, min(ns, G / 2));
+    int ns = 4 * tiles >= 3 * cus ? 1 : target / tiles;
+    ns = max(1, min(ns, G / min_groups));
     pl.gps = cdiv(G, ns);
     pl.nsplit = cdiv(G, pl.gps);
     return pl;
@@ -38,8 +40,9 @@ Plan make_plan(int R, int C, int G, int target) {
 // `prep(args, extra)` runs before the GEMM with `extra_bytes` of scratch
 // (after the split-K partials) and may point args.X / args.xs into it
 template <class CF, bool XS, int OUT, class Prep>
-clove_status_t run(Args a, int target, size_t extra_bytes, hipStream_t stream, Prep prep) {
-    const Plan pl = make_plan<CF>(a.R, a.C, a.G, target);
+clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_bytes, hipStream_t stream,
+                   Prep prep) {
+    const Plan pl = make_plan<CF>(a.R, a.C, a.G, cus, target, min_groups);
     a.tiles_r = pl.tiles_r;
     a.tiles_c = pl.tiles_c;
     a.nsplit = pl.nsplit;
@@ -69,13 +72,20 @@ clove_status_t run(Args a, int target, size_t extra_bytes, hipStream_t stream, P
     return check_launch();
 }
 
+// Tile choice by the number of X rows C (measured on MI355X):
+//   C <= 32: 64 x 32, several workgroups per CU (HBM-bound)
+//   C <= 64, or C >= 256 (W4A16 prefill: the weight tile is re-read per X
+//     tile anyway): 128 x 64 with two workgroups per CU, whose waves
+//     interleave VALU (unpack, fold) with MFMA
+//   otherwise 256 x 128 when it fills the CUs, else 128 x 128 (every weight
+//     row unpacked once per split, which matters while HBM-bound)
 template <bool XS, int OUT, class Prep>
 clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t stream, Prep prep) {
-    if (a.C <= 32) return run<CfgC32, XS, OUT>(a, 2 * cus, extra_bytes, stream, prep);
-    if (a.C <= 64) return run<CfgC64, XS, OUT>(a, cus, extra_bytes, stream, prep);
+    if (a.C <= 32) return run<CfgC32, XS, OUT>(a, cus, 2 * cus, 2, extra_bytes, stream, prep);
+    if (a.C <= 64 || a.C >= 256) return run<CfgC64, XS, OUT>(a, cus, 2 * cus, 8, extra_bytes, stream, prep);
     if (cdiv(a.R, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= cus)
-        return run<CfgBig, XS, OUT>(a, cus, extra_bytes, stream, prep);
-    return run<CfgSq, XS, OUT>(a, cus, extra_bytes, stream, prep);
+        return run<CfgBig, XS, OUT>(a, cus, cus, 2, extra_bytes, stream, prep);
+    return run<CfgSq, XS, OUT>(a, cus, cus, 2, extra_bytes, stream, prep);
 }
 
 bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }

@@ -71,17 +71,24 @@ struct Args {
     unsigned* counters;
 };
 
-template <int WR_, int WC_, int FW_, int FX_, int S_>
+// KS: 16-wide k-steps per stage, 8 (a whole 128-k group) or 4 (half a group:
+// smaller stages, so that two workgroups fit a CU's LDS and each SIMD can
+// interleave two waves; the group is folded after its second stage)
+template <int WR_, int WC_, int FW_, int FX_, int S_, int KS_ = 8>
 struct Cfg {
-    static constexpr int WR = WR_, WC = WC_, FW = FW_, FX = FX_, S = S_;
+    static constexpr int WR = WR_, WC = WC_, FW = FW_, FX = FX_, S = S_, KS = KS_;
     static constexpr int NW = WR * WC, NT = 64 * NW;
     static constexpr int BR = 32 * FW * WR, BC = 32 * FX * WC;
-    static constexpr int X_BYTES = BC * 256, W_BYTES = BR * 64, SC_BYTES = BR * 4;
-    static constexpr int DX = BC / (4 * NW);        // X DMA instructions per thread per stage
-    static constexpr int DW = BR / (16 * NW);       // weight DMA instructions
-    static constexpr int DS = 2 * BR / (64 * NW);   // scale + zero DMA instructions
+    static constexpr int SPG = 8 / KS;                  // stages per group
+    static constexpr int XRB = 32 * KS, WRB = 8 * KS;   // bytes per X row / weight row per stage
+    static constexpr int X_BYTES = BC * XRB, W_BYTES = BR * WRB, SC_BYTES = BR * 4;
+    static constexpr int DX = X_BYTES / (1024 * NW);    // X DMA instructions per thread per stage
+    static constexpr int DW = W_BYTES / (1024 * NW);    // weight DMA instructions
+    static constexpr int DS = 2 * BR / (64 * NW);       // scale + zero DMA instructions
+    static_assert(KS == 8 || KS == 4, "k-steps per stage");
     static_assert(NW == 2 || NW == 4, "waves");
-    static_assert(BC % (4 * NW) == 0 && BR % (16 * NW) == 0 && (2 * BR) % (64 * NW) == 0, "DMA split");
+    static_assert(X_BYTES % (1024 * NW) == 0 && W_BYTES % (1024 * NW) == 0 && (2 * BR) % (64 * NW) == 0,
+                  "DMA split");
     static_assert(BC <= 64 * NW, "one dword of sx per lane covers the tile");
     static_assert(S >= 2 && S <= 4, "stages");
     template <bool XS>
@@ -128,6 +135,13 @@ __device__ __forceinline__ f16x8 unpack8(unsigned w, f16x2 zz) {
     return r;
 }
 
+// weight rows of 64 bytes (whole group) or 32 bytes (half): the 8 lanes of a
+// fragment read (8 consecutive rows, one chunk each) hit 8 bank groups
+template <int KS>
+__device__ __forceinline__ int swz_w(int r) {
+    return KS == 8 ? ((r >> 1) & 3) : ((r >> 2) & 1);
+}
+
 template <int IMM>
 __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt(IMM);
@@ -154,7 +168,8 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     const int tc = tile % p.tiles_c, tr = tile / p.tiles_c;
     const int r0 = tr * BR, c0 = tc * BC;
     const int gbeg = split * p.gps;
-    const int nkt = min(p.G, gbeg + p.gps) - gbeg;
+    constexpr int KS = CF::KS, SPG = CF::SPG;
+    const int nkt = (min(p.G, gbeg + p.gps) - gbeg) * SPG;  // stages of this split
     const int R = p.R, K = p.K, G = p.G;
 
     const unsigned lds0 = __builtin_amdgcn_readfirstlane(
@@ -169,13 +184,15 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     int offx[CF::DX], offw[CF::DW];
 #pragma unroll
     for (int i = 0; i < CF::DX; ++i) {
-        const int row = 4 * (wave * CF::DX + i) + (lane >> 4);
-        offx[i] = (c0 + row) * K * 2 + 16 * ((lane & 15) ^ (row & 7));
+        constexpr int CPR = CF::XRB / 16;  // chunks per X row
+        const int row = (1024 / CF::XRB) * (wave * CF::DX + i) + lane / CPR;
+        offx[i] = (c0 + row) * K * 2 + 16 * ((lane % CPR) ^ (row & 7));
     }
 #pragma unroll
     for (int i = 0; i < CF::DW; ++i) {
-        const int row = 16 * (wave * CF::DW + i) + (lane >> 2);
-        offw[i] = (r0 + row) * (K / 2) + 16 * ((lane & 3) ^ ((row >> 1) & 3));
+        constexpr int CPR = CF::WRB / 16;  // chunks per weight row
+        const int row = (1024 / CF::WRB) * (wave * CF::DW + i) + lane / CPR;
+        offw[i] = (r0 + row) * (K / 2) + 16 * ((lane % CPR) ^ swz_w<KS>(row));
     }
     // scale / zero: instruction j (of 2 BR / 64) covers rows 64 (j % (BR/64)) + lane,
     // scale for j < BR/64, zero otherwise.  Each lane fetches the aligned dword that
@@ -191,12 +208,14 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     if constexpr (XS) rxs = make_rsrc(p.xs, (unsigned)G * p.ldxs * 4);
 
     auto issue = [&](int t, int stage) {
-        const int g = gbeg + t;
+        const int u = gbeg * SPG + t;  // stage index along K
+        const int g = u / SPG;
         const unsigned st = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(stage * SB));
 #pragma unroll
-        for (int i = 0; i < CF::DX; ++i) dma16(rx, st + (wave * CF::DX + i) * 1024, offx[i], g * 256);
+        for (int i = 0; i < CF::DX; ++i) dma16(rx, st + (wave * CF::DX + i) * 1024, offx[i], u * CF::XRB);
 #pragma unroll
-        for (int i = 0; i < CF::DW; ++i) dma16(rw, st + OFF_W + (wave * CF::DW + i) * 1024, offw[i], g * 64);
+        for (int i = 0; i < CF::DW; ++i)
+            dma16(rw, st + OFF_W + (wave * CF::DW + i) * 1024, offw[i], u * CF::WRB);
 #pragma unroll
         for (int i = 0; i < CF::DS; ++i) {
             const int j = wave * CF::DS + i;
@@ -218,10 +237,11 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     const int xrow0 = wc * 32 * FX + l32, wrow0 = wr * 32 * FW + l32;
     unsigned xoff[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) xoff[s] = xrow0 * 256 + 16 * (8 * h + (s ^ (lane & 7)));
-    unsigned woff[2];
+    for (int s = 0; s < KS; ++s) xoff[s] = xrow0 * CF::XRB + 16 * ((KS * h + s) ^ (lane & 7));
+    constexpr int NWC = KS / 4;  // 16-byte weight chunks per lane per stage
+    unsigned woff[NWC];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) woff[e] = OFF_W + wrow0 * 64 + 16 * ((2 * h + e) ^ ((lane >> 1) & 3));
+    for (int e = 0; e < NWC; ++e) woff[e] = OFF_W + wrow0 * CF::WRB + 16 * ((NWC * h + e) ^ swz_w<KS>(wrow0));
     int wrow[FW];
 #pragma unroll
     for (int i = 0; i < FW; ++i) wrow[i] = min(r0 + wrow0 + 32 * i, R - 1);
@@ -243,7 +263,11 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     // stage of tile t (t % S) and of tile t + S - 1 ((t - 1) % S), kept as
     // uniform counters
     int stage = 0, stage_next = S - 1;
-    for (int t = 0; t < nkt; ++t) {
+    f32x16 P[FW][FX];  // the current group's sums (spans SPG stages)
+    for (int t0 = 0; t0 < nkt; t0 += SPG) {
+#pragma unroll
+    for (int hs = 0; hs < SPG; ++hs) {  // stage hs of the group: compile-time in each copy
+        const int t = t0 + hs;
         // stage t landed (everything issued after it may stay in flight), then
         // the barrier: all waves' DMAs of stage t are complete and every wave
         // has finished reading stage t - 1, whose buffer the next issue reuses
@@ -257,7 +281,8 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         const unsigned st = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(stage * SB));
         stage_next = stage;
         stage = stage + 1 == S ? 0 : stage + 1;
-        const int g = gbeg + t;
+        const int g = gbeg + t / SPG;
+        const bool group_first = hs == 0, group_last = hs == SPG - 1;
         // per-lane group scale (x 2^9) and packed -z 2^-9 of the lane's weight rows
         float wsc[FW];
         f16x2 zz[FW];
@@ -273,21 +298,20 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
             const _Float16 nz = (_Float16)(-rintf(h2f(zh)) * (1.0f / 512.0f));
             zz[i] = f16x2{nz, nz};
         }
-        u32x4 wraw[FW][2];
+        u32x4 wraw[FW][NWC];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < NWC; ++e) {
             const unsigned wb = st + woff[e];
 #pragma unroll
-            for (int i = 0; i < FW; ++i) wraw[i][e] = lds_read16(wb + 2048 * i);
+            for (int i = 0; i < FW; ++i) wraw[i][e] = lds_read16(wb + 32 * CF::WRB * i);
         }
 
-        f32x16 P[FW][FX];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < KS; ++s) {
             f16x8 xf[FX], wf[FW];
             const unsigned xb = st + xoff[s];
 #pragma unroll
-            for (int j = 0; j < FX; ++j) xf[j] = bitcast<f16x8>(lds_read16(xb + 8192 * j));
+            for (int j = 0; j < FX; ++j) xf[j] = bitcast<f16x8>(lds_read16(xb + 32 * CF::XRB * j));
 #pragma unroll
             for (int i = 0; i < FW; ++i) {
                 const u32x4& q = wraw[i][s >> 2];
@@ -298,11 +322,12 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
             for (int i = 0; i < FW; ++i)
 #pragma unroll
                 for (int j = 0; j < FX; ++j)
-                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xf[j], wf[i], s == 0 ? zero16 : P[i][j],
-                                                                     0, 0, 0);
+                    P[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        xf[j], wf[i], (s == 0 && group_first) ? zero16 : P[i][j], 0, 0, 0);
         }
 
         // ---- fold the group ----
+        if (!group_last) continue;
         if constexpr (XS) {
 #pragma unroll
             for (int j = 0; j < FX; ++j) {
@@ -330,6 +355,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         }
     }
 
+    }  // stages of one group
     // ---- split-K: publish, the last arriver sums all partials in split order ----
     if (p.nsplit > 1) {
         constexpr int NC = FW * FX * 4;  // f32x4 chunks per thread

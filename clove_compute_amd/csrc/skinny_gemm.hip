@@ -20,6 +20,7 @@ template <class CF, int OUT>
 clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
     a.tiles_m = cdiv(a.M, CF::BM);
     a.tiles_n = cdiv(a.N, CF::BN);
+    a.batch = batch;
     const int tiles = a.tiles_m * a.tiles_n * batch;
     const int nk = a.K / CF::BK;
     // split K (whole K tiles, at least two per split) until about one

@@ -50,7 +50,7 @@ struct Args {
     float alpha, beta;   // kF16AlphaBeta
     int M, N, K;
     int64_t sA, sB, sC;  // batch strides, elements
-    int tiles_m, tiles_n, nsplit, kps;  // kps: K per split (multiple of BK)
+    int tiles_m, tiles_n, batch, nsplit, kps;  // kps: K per split (multiple of BK)
     float* part;
     unsigned* counters;
 };
@@ -70,7 +70,7 @@ struct Cfg {
     static constexpr int D = DA + DB;  // DMA instructions per thread per stage
     static_assert(NW == 4, "four waves");
     static_assert(FM >= 1 && FN >= 1 && BM == 32 * FM * WM && BN == 32 * FN * WN, "wave tiles");
-    static_assert(BNB == 64 || BNB == 128 || BNB == 256, "B row bytes");
+    static_assert(BNB == 64 || BNB == 128 || BNB == 256 || BNB == 512, "B row bytes");
     static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
     static_assert(S >= 2 && S <= 6 && (S - 2) * D <= 63, "stages");
     static constexpr int LDS = S * SB;
@@ -136,8 +136,11 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
     const int wm = wave % CF::WM, wn = wave / CF::WM;
 
     // ---- tile, split, K range ----
-    const int split = blockIdx.x % p.nsplit;
-    int tile = blockIdx.x / p.nsplit;
+    // split-major order: the workgroups in flight together share K rows of B
+    // (whole rows of N are read at once, which keeps HBM pages open)
+    const int ntiles = p.tiles_m * p.tiles_n * p.batch;
+    const int split = blockIdx.x / ntiles;
+    int tile = blockIdx.x - split * ntiles;
     const int per_batch = p.tiles_m * p.tiles_n;
     const int batch = tile / per_batch;
     const int t_in = tile - batch * per_batch;
