@@ -51,6 +51,15 @@ __device__ __forceinline__ unsigned pack2h(float lo, float hi) {
     return static_cast<unsigned>(f2h(lo)) | (static_cast<unsigned>(f2h(hi)) << 16);
 }
 
+// Streaming GEMVs with V weight columns (or token rows): the wide variants
+// (V >= WIDE) and the byte-gathering unaligned ones need more than the 128
+// VGPRs a 1024-thread workgroup leaves, so they run with at most 512 threads
+// (256 VGPRs).
+template <int V, bool ALIGNED, int WIDE>
+__host__ __device__ constexpr int gemv_max_threads() {
+    return (V >= WIDE || !ALIGNED) ? 512 : 1024;
+}
+
 // ---------------------------------------------------------------------------
 // Workgroup barrier for an LDS hand-off only: waits for this wave's LDS
 // operations (lgkmcnt) but not for its global loads still in flight, which

@@ -92,7 +92,7 @@ __device__ __forceinline__ unsigned b_word(const GemvParams& p, int n, int w) {
 // (sA sB) * P.  Literal mode sums (qA - 8)(qB - 8) as int32 over all K.
 // Zero points must lie in [-255, 255] (24-bit products).
 template <int NV, int MODE, int RPW, int UPR, bool ALIGNED>
-__global__ void __launch_bounds__(1024) int4_gemv(GemvParams p) {
+__global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gemv(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
     const int NT = blockDim.x, WPB = NT >> 6;  // UPR: chunks per lane per row per batch
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -327,6 +327,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
 template <int NV, int MODE, int RPW, int UPR>
 clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(NV, p.nch, p.G);
+    wpb = min(wpb, (aligned ? gemv_max_threads<NV, true, 4>() : gemv_max_threads<NV, false, 4>()) / 64);
     const dim3 grid(cdiv(p.M, wpb * RPW));
     auto k = aligned ? int4_gemv<NV, MODE, RPW, UPR, true> : int4_gemv<NV, MODE, RPW, UPR, false>;
     if (lds > 64 * 1024 &&

@@ -49,7 +49,7 @@ __host__ __device__ constexpr int xperm(int k) { return (k & ~7) | ((k & 1) << 2
 // q - z exactly, and v_dot2_f32_f16 with the X pairs accumulates
 // sum_k x_k (q_k - z) in fp32 with exact products; acc += s * that per chunk.
 template <int TV, int RPW, int UPR, bool ALIGNED>
-__global__ void __launch_bounds__(1024) w4a16_gemv(GemvParams p) {
+__global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_gemv(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
     const int NT = blockDim.x, WPB = NT >> 6;  // waves per workgroup (rows / RPW)
     constexpr int XPT = 4;  // X prefetch: 16-byte pieces per thread
@@ -227,6 +227,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
 template <int TV, int RPW, int UPR>
 clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(TV, p.nch);
+    wpb = min(wpb, (aligned ? gemv_max_threads<TV, true, 2>() : gemv_max_threads<TV, false, 2>()) / 64);
     const dim3 grid(cdiv(p.O, wpb * RPW));
     auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true> : w4a16_gemv<TV, RPW, UPR, false>;
     if (lds > 64 * 1024 &&
