@@ -135,9 +135,8 @@ bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t
     auto prep = [&](Args& args, char* extra) -> clove_status_t {
         uint16_t* xt = reinterpret_cast<uint16_t*>(extra);
         float* xs = reinterpret_cast<float*>(extra + xt_bytes);
-        const int64_t threads = (int64_t)(q.K / 8) * (Npad / 2);
-        hipLaunchKernelGGL(i4w_prep_b, dim3((unsigned)cdiv64(threads, 256)), dim3(256), 0, stream, q.B, ldb,
-                           q.B_scale, q.B_zero, q.N, q.K, G, Npad, xt, xs);
+        hipLaunchKernelGGL(i4w_prep_b, dim3((unsigned)G, (unsigned)cdiv(Npad, 128)), dim3(256), 0, stream, q.B,
+                           ldb, q.B_scale, q.B_zero, q.N, q.K, G, Npad, xt, xs);
         args.X = xt;
         args.xs = xs;
         return check_launch();

@@ -424,42 +424,74 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
 // ---------------------------------------------------------------------------
 // B of group-wise INT4 ([K, ldb] bytes, two columns per byte, even n high) ->
 // Xt [Npad, K] fp16 = qB - rint(zB[g, n]) (exact), rows n >= N zero, and
-// xs [G, Npad] fp32 = sB (0 for n >= N).  Thread (n pair j, 8-k block kb);
-// consecutive threads take consecutive k blocks of one row pair, so the
-// 16-byte row stores coalesce.
+// xs [G, Npad] fp32 = sB (0 for n >= N).
+//
+// A workgroup transposes a 128-k (one group) x 64-byte (128-column) tile
+// through LDS: coalesced dword loads of B rows, then thread (column block of
+// 8, k block of 8) reads 8 dwords and writes 8 columns x 8 k as 16-byte rows
+// of Xt.  K % 128 == 0 (checked by the host).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) i4w_prep_b(const uint8_t* __restrict__ B, int ldb,
                                                   const uint16_t* __restrict__ sB,
                                                   const uint16_t* __restrict__ zB, int N, int K, int G,
                                                   int Npad, uint16_t* __restrict__ Xt,
                                                   float* __restrict__ xs) {
-    const int kblocks = K / 8;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)kblocks * (Npad / 2)) return;
-    const int kb = (int)(idx % kblocks), j = (int)(idx / kblocks);
-    const int k0 = 8 * kb, g = k0 / 128;
-    const int n0 = 2 * j, n1 = 2 * j + 1;
-    const bool in0 = n0 < N, in1 = n1 < N;
-    unsigned by[8];
+    __shared__ unsigned tile[128][17];  // 128 k-rows x 16 dwords (+1: conflict-free column reads)
+    const int tid = threadIdx.x;
+    const int g = blockIdx.x, k0 = 128 * g;
+    const int b0 = 64 * blockIdx.y;     // first byte column of the tile (column n = 2 b0)
+    const bool dw = (ldb & 3) == 0 && (reinterpret_cast<uintptr_t>(B) & 3) == 0;
+    // this thread's output columns n0 .. n0 + 7 and k rows 8 k8 .. + 7; their
+    // zero points (and, for k8 == 0, scales) are loaded together with the tile
+    // so that the workgroup makes one round trip to memory
+    const int c8 = tid & 15, k8 = tid >> 4;
+    const int n0 = 2 * b0 + 8 * c8;
+    uint16_t zh[8], sh16[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) by[e] = in0 ? B[(int64_t)(k0 + e) * ldb + j] : 0u;
-    const float z0 = in0 ? rintf(h2f(zB[(int64_t)g * N + n0])) : 0.0f;
-    const float z1 = in1 ? rintf(h2f(zB[(int64_t)g * N + n1])) : 0.0f;
-    unsigned w0[4], w1[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const float a0 = in0 ? (float)(by[2 * d] >> 4) - z0 : 0.0f;
-        const float b0 = in0 ? (float)(by[2 * d + 1] >> 4) - z0 : 0.0f;
-        const float a1 = in1 ? (float)(by[2 * d] & 15u) - z1 : 0.0f;
-        const float b1 = in1 ? (float)(by[2 * d + 1] & 15u) - z1 : 0.0f;
-        w0[d] = pack2h(a0, b0);
-        w1[d] = pack2h(a1, b1);
+    for (int c = 0; c < 8; ++c) {
+        const int n = n0 + c;
+        zh[c] = n < N ? zB[(int64_t)g * N + n] : (uint16_t)0;
+        sh16[c] = (n < N && k8 == 0) ? sB[(int64_t)g * N + n] : (uint16_t)0;
     }
-    *reinterpret_cast<u32x4*>(Xt + (int64_t)n0 * K + k0) = u32x4{w0[0], w0[1], w0[2], w0[3]};
-    *reinterpret_cast<u32x4*>(Xt + (int64_t)n1 * K + k0) = u32x4{w1[0], w1[1], w1[2], w1[3]};
-    if ((kb & 15) == 0) {
-        xs[(int64_t)g * Npad + n0] = in0 ? h2f(sB[(int64_t)g * N + n0]) : 0.0f;
-        xs[(int64_t)g * Npad + n1] = in1 ? h2f(sB[(int64_t)g * N + n1]) : 0.0f;
+    // load: thread t takes row t / 2, dwords 8 (t % 2) .. + 7 of the tile's 64 bytes
+    {
+        const int r = tid >> 1, d0 = 8 * (tid & 1);
+        const uint8_t* row = B + (int64_t)(k0 + r) * ldb;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int bo = b0 + 4 * (d0 + d);
+            unsigned v = 0;
+            if (dw) {
+                if (bo < ldb) v = *reinterpret_cast<const unsigned*>(row + bo);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (bo + e < ldb) v |= (unsigned)row[bo + e] << (8 * e);
+            }
+            tile[r][d0 + d] = v;
+        }
+    }
+    __syncthreads();
+    // transpose: columns n0 .. n0 + 7 are dword c8 of each row
+    if (n0 >= Npad) return;
+    unsigned w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = tile[8 * k8 + i][c8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int n = n0 + c;
+        const bool in = n < N;
+        const float z = in ? rintf(h2f(zh[c])) : 0.0f;
+        const int sh = 8 * (c >> 1) + ((c & 1) ? 0 : 4);  // even column: high nibble
+        unsigned o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = in ? (float)((w[2 * i] >> sh) & 15u) - z : 0.0f;
+            const float b = in ? (float)((w[2 * i + 1] >> sh) & 15u) - z : 0.0f;
+            o[i] = pack2h(a, b);
+        }
+        *reinterpret_cast<u32x4*>(Xt + (int64_t)n * K + k0 + 8 * k8) = u32x4{o[0], o[1], o[2], o[3]};
+        if (k8 == 0) xs[(int64_t)g * Npad + n] = in ? h2f(sh16[c]) : 0.0f;
     }
 }
 
