@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--skip-extra", action="store_true", help="headline only")
+    ap.add_argument("--compare-lib", action="store_true",
+                    help="also time torch.matmul (hipBLASLt) on the headline operands, in blocks "
+                         "alternating with clove_gemm_fp16, and report both")
     return ap.parse_args()
 
 
@@ -134,7 +137,27 @@ def headline(args, timer):
     C = torch.empty(M, N, dtype=torch.float16, device="cuda")
     ms = timer.run(lambda i: cg.gemm_fp16(A, B, C, M, N, K), args.steps, args.warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return dict(ms=ms, tflops=tflops, A=A_h, B=B_h, C=C)
+    return dict(ms=ms, tflops=tflops, A=A_h, B=B_h, C=C, dA=A, dB=B)
+
+
+def compare_library(h, timer, steps, warmup, rounds=3):
+    """torch.matmul (hipBLASLt on ROCm) and clove_gemm_fp16 on the headline's
+    device operands, timed the same way in alternating blocks (the clock drifts
+    with sustained load, so neither side gets a cooler GPU).  TFLOP/s per block."""
+    import torch
+
+    import clove_compute_amd as cg
+
+    A, B, C = h["dA"], h["dB"], h["C"]
+    M, K = A.shape
+    N = B.shape[1]
+    C2 = torch.empty_like(C)
+    tf = lambda ms: 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    out = {"torch_matmul": [], "clove_gemm_fp16": []}
+    for _ in range(rounds):
+        out["torch_matmul"].append(round(tf(timer.run(lambda i: torch.matmul(A, B, out=C2), steps, warmup)), 1))
+        out["clove_gemm_fp16"].append(round(tf(timer.run(lambda i: cg.gemm_fp16(A, B, C, M, N, K), steps, warmup)), 1))
+    return out
 
 
 def cpu_baseline(h, seconds):
@@ -333,8 +356,10 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic, "flops_per_launch": flops,
-                     "kernel": "dma::gemm_f16_dma<Cfg<256,256,64,2,2>>"},
+                     "kernel": "dma::gemm_f16_big<Big>"},
     }
+    if args.compare_lib:
+        line["library_comparison"] = compare_library(h, timer, args.steps, args.warmup)
     if not args.skip_extra:
         line["shapes"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                           for k, v in extras().items()}

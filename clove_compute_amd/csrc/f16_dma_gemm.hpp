@@ -2,41 +2,50 @@
 //
 //   C[M,N] = alpha * A[M,K] @ B[K,N] + beta * C      fp32 accumulation
 //
-// Requirements (checked by the host): K % BK == 0, N % 8 == 0, M >= 1,
-// N >= 8, A/B/C 16-byte aligned, each operand < 2^31 bytes.  Ragged M and N
-// are handled by clamping the load rows/columns (their outputs are never
-// stored).
+// Requirements (checked by the host): K % 64 == 0, N % 8 == 0, M >= 1, N >= 8,
+// A/B/C 16-byte aligned, each operand < 2^31 bytes.  Ragged M and N are
+// handled by the buffer range check (rows past the end of A and B read as
+// zero) and by masking the stores; columns past N inside B's last tile read
+// neighbouring data that only reaches outputs that are never stored.
 //
-// LDS holds both operands K-contiguous per row with the same XOR swizzle,
-//   A stage: [BM rows m][BK k],  B stage: [BN rows n][BK k],
-// 16-byte chunk c of row r at slot c ^ swz(r), so every MFMA fragment is one
-// conflict-free ds_read_b128.  (An LDS read instruction costs the same issue
-// time for 8 and 16 bytes per lane, so the transposing 8-byte reads
-// ds_read_b64_tr_b16 would double the B read cost; LDS issue time is what
-// bounds this kernel.)
+// Tiling.  A 256x256 output tile per workgroup, 4 waves of 128x128, K in tiles
+// of 64.  Each wave's 128x128 is an 8x8 grid of v_mfma_f32_16x16x32_f16: at
+// equal flops this shape reads and writes a quarter of the accumulator bytes
+// of the 32x32x16 form per instruction, and on this part the clock, not the
+// instruction count, bounds a 4096^3 GEMM (the same loop runs ~15 % faster in
+// wall time with it, at the same cycles per flop).
 //
-// Staging.  A (K-contiguous in memory) goes global -> LDS by LDS DMA
-// (buffer_load_dwordx4 ... lds): a wave instruction writes 64 consecutive
-// 16-byte slots and each lane fetches the chunk that belongs in its slot.  B
-// (N-contiguous) is loaded into VGPRs as 8 k-rows x 16 bytes per thread,
-// transposed 8x8 with v_perm_b32 and written as 8 ds_write_b128.
+// Data movement.  Both operands go HBM -> LDS by LDS DMA (buffer_load_dwordx4
+// ... lds): no VGPR staging, no register transpose and no ds_write in the main
+// loop.  A is stored K-contiguous ([m][64 k], 128-byte rows) and its MFMA
+// fragments are ds_read_b128; B stays N-contiguous ([k][256 n], 512-byte rows)
+// and its fragments come from the transposing read ds_read_b64_tr_b16: within
+// a 16-lane group, result lane j element r = source lane 4r + j/4 element
+// j%4, so with source lane s pointing at 8 bytes of k-row kb + s/4, columns
+// 4(s%4)..+3, every lane receives 4 consecutive k of one column; two such
+// reads make the 8-k operand.  Both layouts XOR-swizzle their 16-byte chunks
+// so that every fragment read is bank-conflict free:
+//   A row r: chunk c at slot c ^ (r % 8) ^ ((r / 8) % 2)
+//   B row r: chunk c at slot c ^ 2 (r % 4)
 //
-// MFMA: v_mfma_f32_32x32x16_f16 with the B tile as the MFMA "A" operand
-// (rows = n) and the A tile as the MFMA "B" operand (cols = m); a lane holds
-// 8 consecutive k of one row for both.  Each wave owns WTM x WTN outputs.
+// Pipeline.  LDS holds three A stages and two B stages (160 KB).  Tile kt's A
+// arrives during tile kt-2, its B during tile kt-1 right after that tile's
+// barrier (which frees the B stage of tile kt-1); one workgroup barrier per K
+// tile, three quarters of the way through it.  MFMAs, fragment reads and DMAs
+// follow a fixed slot plan (kPlan below): one LDS read every 2-3 MFMAs, so the
+// LDS pipe, shared by the four waves, runs at an even ~75 % instead of in
+// bursts.  DMA completion is tracked with explicit vmcnt waits (the DMAs are
+// inline asm, so the compiler neither waits for them before every LDS read nor
+// counts them).
 //
-// Pipeline.  LDS holds three A stages and two B stages (160 KB).  During K
-// tile t the thread writes the transposed B of tile t+1 from VGPRs (spread
-// over the first k-steps), then loads the B rows of tile t+2 into the same
-// VGPRs and issues the A DMA of tile t+2.  The A DMA is inline asm with explicit vmcnt
-// waits, since the compiler would otherwise wait for every DMA in flight
-// before any LDS read.  One barrier per K tile, placed mid-way through the last
-// k-step so that its second half hides the first fragment reads of the next
-// tile.  MFMAs, fragment reads and memory instructions are interleaved in a
-// fixed order (sched_barrier) that never queues more than one LDS write or
-// memory instruction per MFMA.
+// Accumulators.  The MFMAs are inline asm with the accumulator tied in place
+// ("+a"): the compiler's own MFMA selection copied accumulator tuples between
+// registers around the unrolled loop (hundreds of v_accvgpr moves per tile).
+// Since the compiler does not see these as MFMAs, the kernel inserts the
+// wait states its hazard recognizer would: before the first MFMA reads the
+// zeroed accumulators and after the last MFMA, before they are read.
 //
-// Epilogue (beta == 0): the wave's fp16 tile goes through LDS so that every
+// Epilogue (beta == 0): each wave's fp16 tile goes through LDS so that every
 // global store is a full 16-byte lane of a contiguous row segment.
 #pragma once
 
@@ -47,8 +56,6 @@ namespace dma {
 
 using namespace hw;
 
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-
 struct Args {
     const uint16_t* A;
     const uint16_t* B;
@@ -58,33 +65,6 @@ struct Args {
     int64_t sA, sB, sC;  // batch strides (elements)
     int tiles_m, tiles_n;
 };
-
-template <int BM_, int BN_, int BK_, int WGM_, int WGN_>
-struct Cfg {
-    static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
-    static constexpr int NW = WGM * WGN, NT = NW * 64;
-    static constexpr int WTM = BM / WGM, WTN = BN / WGN;
-    static constexpr int FM = WTM / 32, FN = WTN / 32;
-    static constexpr int KSTEPS = BK / 16;
-    static constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
-    static constexpr int DMA_A = A_ELEMS / 8 / NT;  // A DMA instructions per thread per K tile
-    static constexpr int CPR = BK / 8;              // 16-byte chunks per LDS row
-    static constexpr int A_STAGES = 3, B_STAGES = 2;
-    static constexpr size_t LDS_BYTES = (size_t)(A_STAGES * A_ELEMS + B_STAGES * B_ELEMS) * 2;
-    static_assert(LDS_BYTES <= 163840, "LDS");
-    static_assert(NW * WTM * (WTN * 2 + 16) <= (int)LDS_BYTES, "epilogue staging");
-    static_assert(BK == 64, "K tile (swizzle, 8-row B blocks)");
-    static_assert(A_ELEMS % (8 * NT) == 0 && 64 % CPR == 0, "A DMA split");
-    static_assert((BK / 8) * (BN / 8) == NT, "one 8x8 B block per thread");
-    static_assert(WTM % 32 == 0 && WTN % 32 == 0 && KSTEPS % 2 == 0, "wave tile");
-    static_assert(FM * FN >= 2 * (FM + FN) && FM * FN % 2 == 0, "slots for reads and B writes");
-};
-
-template <int BK>
-__device__ __forceinline__ int swz_a(int r) {
-    if constexpr (BK == 64) return (r + (r >> 3)) & 7;
-    else return ((r >> 1) + (r >> 3)) & 3;
-}
 
 // s_waitcnt with only the vector-memory counter constrained
 __host__ __device__ constexpr int vmcnt_imm(int n) {
@@ -132,7 +112,105 @@ struct IntC {
     static constexpr int value = V;
 };
 
-template <class CF>
+// ---------------------------------------------------------------------------
+// Tile configuration and slot plan
+// ---------------------------------------------------------------------------
+struct Big {
+    static constexpr int BM = 256, BN = 256, BK = 64, NW = 4, NT = 256;
+    static constexpr int WTM = 128, WTN = 128, FM = 8, FN = 8;  // 16x16 fragments per wave
+    static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+    static constexpr int A_STAGES = 3, B_STAGES = 2;
+    static constexpr int LDS_BYTES = A_STAGES * A_BYTES + B_STAGES * B_BYTES;
+    static constexpr int DMA_A = A_BYTES / 1024 / NW, DMA_B = B_BYTES / 1024 / NW;  // per wave per tile
+    static_assert(LDS_BYTES <= 163840, "LDS");
+    static_assert(NW * WTM * (WTN * 2 + 16) <= LDS_BYTES, "epilogue staging");
+    static_assert(DMA_A == 8 && DMA_B == 8, "slot plan");
+};
+
+// A K tile is 128 MFMA slots: k-step 0 (32 k) in slots 0..63, k-step 1 in
+// 64..127; MFMA n of a k-step is tile (i = n / 8, j = n % 8), B fragment i x
+// A fragment j.  Registers: fa[s][8] (A, one set per k-step) and fb[8] (B,
+// two halves each) refilled as slots free them: fb[i] is last used at slot
+// 8i + 7 of each k-step.  The barrier sits before slot kBar.
+enum ReadKind : int {
+    kA1 = 1,   // fa[1][i]: A, k-step 1 of this tile
+    kB1 = 2,   // fb[i] half e: B, k-step 1 of this tile
+    kB0 = 3,   // fb[i] half e: B, k-step 0 of this tile (still in use at the previous barrier)
+    kA0n = 4,  // fa[0][i]: A, k-step 0 of the next tile (after the barrier)
+    kB0n = 5,  // fb[i] half e: B, k-step 0 of the next tile (after the barrier)
+};
+struct ReadSlot {
+    int slot, kind, i, e;
+};
+constexpr int kBar = 96;
+// 48 LDS reads per wave per tile, evenly spaced (one per 2-3 MFMAs), each no
+// earlier than its register frees and at least 8 slots before its first use
+constexpr ReadSlot kReads[48] = {
+    {0, kB0, 2, 0}, {2, kB0, 2, 1}, {5, kB0, 3, 0}, {8, kB0, 3, 1}, {10, kB0, 4, 0},
+    {13, kB0, 4, 1}, {16, kB0, 5, 0}, {18, kB0, 5, 1}, {21, kB0, 6, 0}, {24, kB0, 6, 1},
+    {26, kB0, 7, 0}, {29, kB0, 7, 1}, {32, kA1, 0, 0}, {34, kB1, 0, 0}, {37, kB1, 0, 1},
+    {40, kA1, 1, 0}, {42, kA1, 2, 0}, {45, kA1, 3, 0}, {48, kA1, 4, 0}, {50, kA1, 5, 0},
+    {53, kA1, 6, 0}, {56, kA1, 7, 0}, {58, kB1, 1, 0}, {61, kB1, 1, 1}, {64, kB1, 2, 0},
+    {66, kB1, 2, 1}, {69, kB1, 3, 0}, {72, kB1, 3, 1}, {74, kB1, 4, 0}, {77, kB1, 4, 1},
+    {80, kB1, 5, 0}, {82, kB1, 5, 1}, {85, kB1, 6, 0}, {88, kB1, 6, 1}, {90, kB1, 7, 0},
+    {93, kB1, 7, 1}, {96, kA0n, 0, 0}, {98, kB0n, 0, 0}, {101, kB0n, 0, 1},
+    {104, kA0n, 1, 0}, {106, kA0n, 2, 0}, {109, kA0n, 3, 0}, {112, kA0n, 4, 0},
+    {114, kA0n, 5, 0}, {117, kA0n, 6, 0}, {120, kA0n, 7, 0}, {122, kB0n, 1, 0},
+    {125, kB0n, 1, 1}};
+
+// DMAs per tile: A of tile kt+2 before the barrier, B of tile kt+2 after it
+// (into the B stage the barrier just freed)
+__host__ __device__ constexpr int plan_dma_a(int g) { return (g >= 4 && g < kBar && (g - 4) % 12 == 0) ? (g - 4) / 12 : -1; }
+__host__ __device__ constexpr int plan_dma_b(int g) { return (g >= 98 && (g - 98) % 4 == 0) ? (g - 98) / 4 : -1; }
+// At the barrier of tile kt, A(kt+1) and B(kt+1) (issued during tile kt-1,
+// B last) must have landed: only this tile's A DMAs may still be in flight.
+constexpr int kWaitBar = 8;
+
+struct PlanTable {
+    short op[128];  // kind * 32 + i * 2 + e, or -1
+};
+constexpr PlanTable make_plan_table() {
+    PlanTable t{};
+    for (int g = 0; g < 128; ++g) t.op[g] = -1;
+    for (const ReadSlot& r : kReads) t.op[r.slot] = (short)(r.kind * 32 + r.i * 2 + r.e);
+    return t;
+}
+constexpr PlanTable kPlan = make_plan_table();
+
+// Every fragment read exactly once per tile, each inside its window; the DMA
+// plan issues 8 + 8 per tile with the A DMAs before the barrier and the B
+// DMAs after it.
+constexpr bool plan_valid() {
+    int seen[6][8][2] = {};
+    int slots[128] = {};
+    for (const ReadSlot& r : kReads) {
+        if (r.slot < 0 || r.slot >= 128 || slots[r.slot]++) return false;
+        if (r.i < 0 || r.i >= 8 || r.e < 0 || r.e > 1) return false;
+        seen[r.kind][r.i][r.e]++;
+        const int s = r.slot, i = r.i;
+        switch (r.kind) {
+            case kA1: if (r.e != 0 || s > 64 + i - 8) return false; break;
+            case kB1: if (s < 8 * i + 8 || s > 64 + 8 * i - 8) return false; break;
+            case kB0: if (i < 2 || s > 8 * i - 8) return false; break;
+            case kA0n: if (r.e != 0 || s < kBar || s > 128 + i - 6) return false; break;
+            case kB0n: if (i >= 2 || s < kBar || s < 64 + 8 * i + 8 || s > 128 + 8 * i - 6) return false; break;
+            default: return false;
+        }
+    }
+    for (int i = 0; i < 8; ++i) {
+        if (seen[kA1][i][0] != 1 || seen[kA0n][i][0] != 1) return false;
+        for (int e = 0; e < 2; ++e)
+            if (seen[kB1][i][e] != 1 || seen[i < 2 ? kB0n : kB0][i][e] != 1) return false;
+    }
+    int na = 0, nb = 0;
+    for (int g = 0; g < 128; ++g) {
+        if (plan_dma_a(g) >= 0) { if (g >= kBar || plan_dma_a(g) != na) return false; ++na; }
+        if (plan_dma_b(g) >= 0) { if (g <= kBar || plan_dma_b(g) != nb) return false; ++nb; }
+    }
+    return na == Big::DMA_A && nb == Big::DMA_B && na == kWaitBar;
+}
+static_assert(plan_valid(), "slot plan");
+
 __device__ __forceinline__ void tile_coords(const Args& p, int& batch, int& tm, int& tn) {
     int bid = blockIdx.x;
     const int nblk = gridDim.x;
@@ -151,204 +229,184 @@ __device__ __forceinline__ void tile_coords(const Args& p, int& batch, int& tm, 
     tn = in_group / gm;
 }
 
+typedef short i16x4v __attribute__((vector_size(8)));
+typedef __attribute__((address_space(3))) i16x4v lds_i16x4v;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+
+// The accumulators as inline-asm operands, 8 tiles at a time: the wait states
+// (s_nop) a VALU write / MFMA result needs before the next reader, placed
+// where the compiler cannot move the readers or writers across them.
+template <int NOPS>
+__device__ __forceinline__ void acc_fence(f32x4 (&acc)[64]) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        f32x4* a = acc + 8 * g;
+        if (g == 0 && NOPS > 0)
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+a"(a[0]), "+a"(a[1]), "+a"(a[2]), "+a"(a[3]), "+a"(a[4]), "+a"(a[5]), "+a"(a[6]), "+a"(a[7]));
+        else
+            asm volatile("s_nop 1"
+                         : "+a"(a[0]), "+a"(a[1]), "+a"(a[2]), "+a"(a[3]), "+a"(a[4]), "+a"(a[5]), "+a"(a[6]), "+a"(a[7]));
+    }
+}
+
+// (a template so that every translation unit that includes this header can
+// see it without defining the kernel twice; launched as gemm_f16_big<Big>)
 template <class CF>
-__global__ void __launch_bounds__(CF::NT) gemm_f16_dma(Args p) {
-    constexpr int BM = CF::BM, BN = CF::BN, BK = CF::BK, NW = CF::NW;
-    constexpr int FM = CF::FM, FN = CF::FN, KSTEPS = CF::KSTEPS;
-    constexpr int A_BYTES = CF::A_ELEMS * 2, B_BYTES = CF::B_ELEMS * 2;
-    constexpr int NMF = FM * FN;    // MFMAs per k-step
-    constexpr int NR = FM + FN;     // fragment reads per k-step
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[CF::LDS_BYTES / 2];
+__global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
+    using Big = CF;
+    constexpr int BM = Big::BM, BN = Big::BN, BK = Big::BK, NW = Big::NW;
+    constexpr int WTM = Big::WTM, WTN = Big::WTN, FM = Big::FM, FN = Big::FN;
+    constexpr int A_BYTES = Big::A_BYTES, B_BYTES = Big::B_BYTES;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[Big::LDS_BYTES / 2];
 
     int batch, tm, tn;
-    tile_coords<CF>(p, batch, tm, tn);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
+    tile_coords(p, batch, tm, tn);
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / CF::WGN, wn = wave % CF::WGN;
+    const int wm = wave >> 1, wn = wave & 1;
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
     const int KT = K / BK;
 
     const u32x4 ra = make_rsrc(p.A + batch * p.sA, (unsigned)M * K * 2);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(p.B + batch * p.sB), (short)0, K * N * 2, 0x00020000);
+    const u32x4 rb = make_rsrc(p.B + batch * p.sB, (unsigned)K * N * 2);
     const unsigned lds_base = __builtin_amdgcn_readfirstlane(
         (unsigned)(size_t)((__attribute__((address_space(3))) uint16_t*)smem));
-    const unsigned lds_a = lds_base, lds_b = lds_base + CF::A_STAGES * A_BYTES;
+    const unsigned lds_a = lds_base, lds_b = lds_base + Big::A_STAGES * A_BYTES;
 
-    // Swizzle arithmetic.  For a row r = 32 x + (lane % 32) (x any integer)
-    // swz(r) = (r + r/8) % 8 = (s0 + 4 x) % 8 = s0 ^ (4 (x % 2)), with
-    // s0 = (lane % 8 + (lane / 8) % 4) % 8, so every fragment address is a
-    // per-lane value plus a constant.
-    static_assert(BM == 256 && BN == 256 && NW == 4 && CF::WTM == 128 && CF::WTN == 128,
-                  "address arithmetic below is written for 256x256x64 with 2x2 waves");
-
-    // ---- A: LDS DMA.  Instruction i of wave w fills rows 32 i + 8 w + lane/8,
-    // slot lane % 8; rows >= M read as zero through the buffer range check ----
-    const int dsw = ((lane >> 3) + wave) & 7;  // swz of the DMA row, for even i
-    int offA[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-        offA[e] = 2 * ((m0 + 8 * wave + (lane >> 3)) * K + 8 * ((lane & 7) ^ dsw ^ (4 * e)));
+    // ---- A DMA: instruction i of wave w fills rows 32 i + 8 w + lane / 8,
+    // slot lane % 8, which holds global chunk slot ^ swz(row) ----
+    const int offA = 2 * ((m0 + 8 * wave + (lane >> 3)) * K + 8 * ((lane & 7) ^ (lane >> 3) ^ (wave & 1)));
     auto dma_a = [&](int kt, int ast, int i) {
-        dma16(ra, lds_a + ast * A_BYTES + (i * NW + wave) * 1024, offA[i & 1],
-              kt * BK * 2 + i * 32 * K * 2);
+        dma16(ra, lds_a + ast * A_BYTES + (i * NW + wave) * 1024, offA, kt * BK * 2 + i * 32 * K * 2);
+    };
+    // ---- B DMA: instruction i of wave w fills k-rows 8 i + 2 w + lane / 32,
+    // slot lane % 32 (512-byte rows) ----
+    const int rB = 2 * wave + (lane >> 5);
+    const int offB = 2 * (rB * N + n0) + 16 * ((lane & 31) ^ (2 * (rB & 3)));
+    auto dma_b = [&](int kt, int bst, int i) {
+        dma16(rb, lds_b + bst * B_BYTES + (8 * i + 2 * wave) * 512, offB, (kt * BK + 8 * i) * N * 2);
     };
 
-    // ---- B: thread owns k-rows 8kb..8kb+7 x columns 8cb..8cb+7 of the tile ----
-    const int cb = tid % (BN / 8), kb = tid / (BN / 8);
-    const int offB = 2 * (8 * kb * N + min(n0 + 8 * cb, N - 8));
-    u32x4 breg[8];
-    // compiler-visible loads: the compiler inserts the vmcnt wait before each
-    // use (counting only these loads, so it may also wait for A DMAs issued in
-    // between, which is safe)
-    auto load_b = [&](int kt, int rr) {
-        breg[rr] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rb, offB, (kt * BK + rr) * N * 2, 0));
+    // ---- A fragment x of k-step s: row 16 x + q, chunk 4 s + h, at slot
+    // (4 s + h) ^ (q % 8) ^ (q / 8) (q = lane % 16, h = lane / 16) ----
+    const int q = lane & 15, h = lane >> 4;
+    unsigned fo[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) fo[s] = wm * WTM * BK * 2 + q * BK * 2 + 16 * ((4 * s + h) ^ (q & 7) ^ (q >> 3));
+    auto rd_a = [&](int ast, int s, int x) -> f16x8 {
+        return bitcast<f16x8>(
+            *reinterpret_cast<const lds_u32x4*>((size_t)(lds_a + ast * A_BYTES + fo[s] + x * 16 * BK * 2)));
     };
-    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-    // column c of the 8x8 block: 8 k-values, two per dword, from the 8 loaded
-    // rows, written to B^T row n = 8cb + c, chunk kb (swz(n) = (c + cb) % 8)
-    auto write_b = [&](int bst, int c) {
-        const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
-        const int d = c >> 1;
-        const u32x4(&r)[8] = breg;
-        u32x4 w;
-        w.x = __builtin_amdgcn_perm(r[1][d], r[0][d], sel);
-        w.y = __builtin_amdgcn_perm(r[3][d], r[2][d], sel);
-        w.z = __builtin_amdgcn_perm(r[5][d], r[4][d], sel);
-        w.w = __builtin_amdgcn_perm(r[7][d], r[6][d], sel);
-        const unsigned off = (8 * cb + c) * BK * 2 + 16 * (kb ^ ((c + cb) & 7));
-        *reinterpret_cast<lds_u32x4*>((size_t)(lds_b + bst * B_BYTES + off)) = w;
+    // ---- B fragment i (columns wn 128 + 16 i ..), k-step s, half e: source lane
+    // q of group h points at k-row 32 s + 8 h + 4 e + q / 4, columns + 4 (q % 4);
+    // its slot (chunk ^ 2 (q / 4)) depends on i % 4 only, i / 4 adds 128 bytes ----
+    const int t4 = q >> 2;
+    unsigned tb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        tb[u] = (8 * h + t4) * 512 + 16 * (wn * 16 + ((2 * u + ((q & 3) >> 1)) ^ (2 * t4))) + 8 * (q & 1);
+    auto rd_b = [&](unsigned base, int s, int i, int e) -> u32x2 {
+        const unsigned a = base + tb[i & 3] + (32 * s + 4 * e) * 512 + 128 * (i >> 2);
+        return bitcast<u32x2>(__builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4v*>((size_t)a)));
     };
 
-    // ---- fragment reads: row 32 x + lane % 32 of the wave tile, chunk 2t + lane/32 ----
-    const int s0 = ((lane & 7) + ((lane >> 3) & 3)) & 7;
-    unsigned foff[KSTEPS][2];  // [t][x % 2]
+    f32x4 acc[FN * FM];  // tile (i, j) at 8 i + j
 #pragma unroll
-    for (int t = 0; t < KSTEPS; ++t)
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-            foff[t][e] = (lane & 31) * BK * 2 + 16 * (((2 * t + (lane >> 5)) ^ s0) ^ (4 * e));
-    auto read_one = [&](int r, int ast, int bst, int t, f16x8 (&fa)[FM], f16x8 (&fb)[FN]) {
-        if (r < FM) {
-            const unsigned a = lds_a + ast * A_BYTES + wm * CF::WTM * BK * 2 + r * 32 * BK * 2 + foff[t][r & 1];
-            fa[r] = bitcast<f16x8>(*reinterpret_cast<const lds_u32x4*>((size_t)a));
-        } else {
-            const int i = r - FM;
-            const unsigned a = lds_b + bst * B_BYTES + wn * CF::WTN * BK * 2 + i * 32 * BK * 2 + foff[t][i & 1];
-            fb[i] = bitcast<f16x8>(*reinterpret_cast<const lds_u32x4*>((size_t)a));
-        }
-    };
+    for (int n = 0; n < FN * FM; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f16x8 fa[2][FM];
+    u32x2 fb[FN][2];
 
-    f32x16 acc[FN][FM];
+    // ---- prologue: A(0), B(0), A(1), B(1) in flight in that order (the waits
+    // below count on it), the first two landed, k-step 0 fragments of tile 0 ----
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+    for (int i = 0; i < Big::DMA_A; ++i) dma_a(0, 0, i);
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-    auto mfma = [&](int n, const f16x8 (&fa)[FM], const f16x8 (&fb)[FN]) {
-        const int i = n / FM, j = n % FM;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[i], fa[j], acc[i][j], 0, 0, 0);
-    };
-
-    // ---- prologue: B^T of tile 0 written, B rows of tile 1 in VGPRs, A tiles 0, 1 in flight ----
-    // per K tile the issue order is: 8 B row loads, then the A DMA
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) load_b(0, rr);
-#pragma unroll
-    for (int i = 0; i < CF::DMA_A; ++i) dma_a(0, 0, i);
-#pragma unroll
-    for (int c = 0; c < 8; ++c) write_b(0, c);
+    for (int i = 0; i < Big::DMA_B; ++i) dma_b(0, 0, i);
     const int k1 = min(1, KT - 1);
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) load_b(k1, rr);
+    for (int i = 0; i < Big::DMA_A; ++i) dma_a(k1, 1, i);
 #pragma unroll
-    for (int i = 0; i < CF::DMA_A; ++i) dma_a(k1, 1, i);
-    stage_barrier<vmcnt_imm(8 + CF::DMA_A)>();  // A tile 0 (16 later ops) and B^T tile 0
-
-    f16x8 fa[2][FM], fb[2][FN];
+    for (int i = 0; i < Big::DMA_B; ++i) dma_b(k1, 1, i);
+    stage_barrier<vmcnt_imm(Big::DMA_A + Big::DMA_B)>();
 #pragma unroll
-    for (int r = 0; r < NR; ++r) read_one(r, 0, 0, 0, fa[0], fb[0]);
-
-    int ast = 0;   // A stage of tile kt
-    int bst = 0;   // B stage of tile kt
-    // Slot plan over k-steps 0 .. KSTEPS-2 (slot g = NMF t + n; fragment
-    // reads of k-step t+1 occupy n < NR of every k-step): the 8 transposed B
-    // writes of tile kt+1 at g = 8..15, then (their registers read) the 8 B
-    // row loads of tile kt+2 at g = 16..23 and its A DMA from g = 24.
-    constexpr int NG = NMF * (KSTEPS - 1);
-    static_assert(NMF == 16 && NR == 8 && NG >= 24 + CF::DMA_A, "slot plan");
-#pragma unroll 1
-    for (int kt = 0; kt < KT; ++kt) {
-        const int ast1 = ast == 2 ? 0 : ast + 1;    // tile kt+1
-        const int ast2 = ast1 == 2 ? 0 : ast1 + 1;  // tile kt+2 (read last during tile kt-1)
-        const int bst1 = bst ^ 1;
-        const int k2 = min(kt + 2, KT - 1);
-#pragma unroll
-        for (int t = 0; t < KSTEPS - 1; ++t) {
-            const int cur = t & 1;
-#pragma unroll
-            for (int n = 0; n < NMF; ++n) {
-                const int g = NMF * t + n;
-                mfma(n, fa[cur], fb[cur]);
-                if (n < NR) read_one(n, ast, bst, t + 1, fa[cur ^ 1], fb[cur ^ 1]);
-                if (g >= 8 && g < 16) write_b(bst1, g - 8);
-                if (g >= 16 && g < 24) load_b(k2, g - 16);
-                if (g >= 24 && g - 24 < CF::DMA_A) dma_a(k2, ast2, g - 24);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        {
-            constexpr int cur = (KSTEPS - 1) & 1;
-#pragma unroll
-            for (int n = 0; n < NMF / 2; ++n) {
-                mfma(n, fa[cur], fb[cur]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // A of tile kt+1 landed (the 8 + DMA_A ops of tile kt+2 may be in
-            // flight), B^T of tile kt+1 written, stage of tile kt-1 free
-            stage_barrier<vmcnt_imm(8 + CF::DMA_A)>();
-#pragma unroll
-            for (int n = NMF / 2; n < NMF; ++n) {
-                mfma(n, fa[cur], fb[cur]);
-                const int r = n - NMF / 2;
-                if (r < NR) read_one(r, ast1, bst1, 0, fa[cur ^ 1], fb[cur ^ 1]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int r = NMF / 2; r < NR; ++r) read_one(r, ast1, bst1, 0, fa[cur ^ 1], fb[cur ^ 1]);
-        }
-        ast = ast1;
-        bst = bst1;
+    for (int x = 0; x < 8; ++x) {
+        fa[0][x] = rd_a(0, 0, x);
+        fb[x][0] = rd_b(lds_b, 0, x, 0);
+        fb[x][1] = rd_b(lds_b, 0, x, 1);
     }
-    // every load has landed and every wave is done with the stages
+    acc_fence<0>(acc);  // the zeroed accumulators are written before the first MFMA reads them
+
+    int ast = 0;  // A stage of the current tile (tiles rotate through 3)
+    // tile kt with parity P: B stage P holds it, B stage P ^ 1 the next tile
+    auto tile = [&](int kt, auto PC) {
+        constexpr int P = decltype(PC)::value;
+        const int ast1 = ast == 2 ? 0 : ast + 1;
+        const int ast2 = ast1 == 2 ? 0 : ast1 + 1;
+        const int k2 = min(kt + 2, KT - 1);
+        // opaque per tile, so the B read addresses fold into instruction offsets
+        unsigned bcur = lds_b + P * B_BYTES, bnext = lds_b + (P ^ 1) * B_BYTES;
+        asm volatile("" : "+v"(bcur), "+v"(bnext));
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int n = 0; n < 64; ++n) {
+                const int g = 64 * s + n;
+                if (g == kBar) stage_barrier<vmcnt_imm(kWaitBar)>();
+                {
+                    const int i = n >> 3, j = n & 7;
+                    const u32x4 bf = {fb[i][0].x, fb[i][0].y, fb[i][1].x, fb[i][1].y};
+                    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                                 : "+a"(acc[n])
+                                 : "v"(bitcast<f16x8>(bf)), "v"(fa[s][j]));
+                }
+                const int op = kPlan.op[g];
+                if (op >= 0) {
+                    const int kind = op >> 5, x = (op >> 1) & 15, e = op & 1;
+                    if (kind == kA1) fa[1][x] = rd_a(ast, 1, x);
+                    else if (kind == kB1) fb[x][e] = rd_b(bcur, 1, x, e);
+                    else if (kind == kB0) fb[x][e] = rd_b(bcur, 0, x, e);
+                    else if (kind == kA0n) fa[0][x] = rd_a(ast1, 0, x);
+                    else fb[x][e] = rd_b(bnext, 0, x, e);
+                }
+                if (plan_dma_a(g) >= 0) dma_a(k2, ast2, plan_dma_a(g));
+                if (plan_dma_b(g) >= 0) dma_b(k2, P, plan_dma_b(g));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        ast = ast1;
+    };
+    int kt = 0;
+#pragma unroll 1
+    for (; kt + 1 < KT; kt += 2) {
+        tile(kt, IntC<0>{});
+        tile(kt + 1, IntC<1>{});
+    }
+    if (kt < KT) tile(kt, IntC<0>{});  // odd K / 64
+    // every DMA has landed and every wave is done with the stages
     stage_barrier<vmcnt_imm(0)>();
+    acc_fence<1>(acc);  // the last MFMA results land before the accumulators are read
 
     uint16_t* C = p.C + batch * p.sC;
-    const int wrow0 = m0 + wm * CF::WTM, wcol0 = n0 + wn * CF::WTN;
+    const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
+    // lane holds m = 16 j + q, n = 16 i + 4 h + 0..3 of tile (i, j)
     if (p.beta == 0.0f) {
-        // ---- epilogue through LDS: lane holds m = 32j + l%32, n = 32i + 8q + 4(l/32) + 0..3 ----
-        constexpr int PITCH = CF::WTN * 2 + 16;  // bytes; the pad spreads rows over the banks
-        const unsigned wbase = lds_base + wave * CF::WTM * PITCH;
+        constexpr int PITCH = WTN * 2 + 16;  // bytes; the pad spreads rows over the banks
+        const unsigned wbase = lds_base + wave * WTM * PITCH;
 #pragma unroll
         for (int j = 0; j < FM; ++j)
 #pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int m = 32 * j + (lane & 31), n = 32 * i + 8 * q + 4 * (lane >> 5);
-                    const u32x2 v = {pack2h(p.alpha * acc[i][j][4 * q], p.alpha * acc[i][j][4 * q + 1]),
-                                     pack2h(p.alpha * acc[i][j][4 * q + 2], p.alpha * acc[i][j][4 * q + 3])};
-                    *reinterpret_cast<__attribute__((address_space(3))) u32x2*>(
-                        (size_t)(wbase + m * PITCH + n * 2)) = v;
-                }
+            for (int i = 0; i < FN; ++i) {
+                const f32x4 v = acc[8 * i + j];
+                const u32x2 w = {pack2h(p.alpha * v[0], p.alpha * v[1]), pack2h(p.alpha * v[2], p.alpha * v[3])};
+                *reinterpret_cast<lds_u32x2*>((size_t)(wbase + (16 * j + q) * PITCH + (16 * i + 4 * h) * 2)) = w;
+            }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes are visible to its reads
-        constexpr int CPRW = CF::WTN / 8;      // 16-byte chunks per row of the wave tile
+        constexpr int CPRW = WTN / 8;          // 16-byte chunks per row of the wave tile
         constexpr int RPI = 64 / CPRW;         // rows per store instruction
 #pragma unroll
-        for (int it = 0; it < CF::WTM / RPI; ++it) {
+        for (int it = 0; it < WTM / RPI; ++it) {
             const int m = it * RPI + lane / CPRW, c = lane % CPRW;
             const u32x4 v = *reinterpret_cast<const lds_u32x4*>((size_t)(wbase + m * PITCH + c * 16));
             const int gm = wrow0 + m, gn = wcol0 + 8 * c;
@@ -359,24 +417,20 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_dma(Args p) {
     // ---- epilogue with beta: read-modify-write straight from the accumulators ----
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
-        const int gm = wrow0 + 32 * j + (lane & 31);
+        const int gm = wrow0 + 16 * j + q;
         if (gm >= M) continue;
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int gn = wcol0 + 32 * i + 8 * q + 4 * (lane >> 5);
-                if (gn >= N) continue;
-                float r0 = p.alpha * acc[i][j][4 * q], r1 = p.alpha * acc[i][j][4 * q + 1];
-                float r2 = p.alpha * acc[i][j][4 * q + 2], r3 = p.alpha * acc[i][j][4 * q + 3];
-                uint16_t* dst = C + (int64_t)gm * N + gn;
-                const u32x2 c = *reinterpret_cast<const u32x2*>(dst);
-                r0 = fmaf(p.beta, h2f(c.x & 0xffffu), r0);
-                r1 = fmaf(p.beta, h2f(c.x >> 16), r1);
-                r2 = fmaf(p.beta, h2f(c.y & 0xffffu), r2);
-                r3 = fmaf(p.beta, h2f(c.y >> 16), r3);
-                *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r0, r1), pack2h(r2, r3)};
-            }
+            const int gn = wcol0 + 16 * i + 4 * h;
+            if (gn >= N) continue;
+            const f32x4 v = acc[8 * i + j];
+            uint16_t* dst = C + (int64_t)gm * N + gn;
+            const u32x2 c = *reinterpret_cast<const u32x2*>(dst);
+            const float r0 = fmaf(p.beta, h2f(c.x & 0xffffu), p.alpha * v[0]);
+            const float r1 = fmaf(p.beta, h2f(c.x >> 16), p.alpha * v[1]);
+            const float r2 = fmaf(p.beta, h2f(c.y & 0xffffu), p.alpha * v[2]);
+            const float r3 = fmaf(p.beta, h2f(c.y >> 16), p.alpha * v[3]);
+            *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r0, r1), pack2h(r2, r3)};
         }
     }
 }

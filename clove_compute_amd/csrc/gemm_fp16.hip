@@ -3,9 +3,9 @@
 // Replaces the reference's gemm_fp16 (src/kernels/gemm_fp16.cu:277-305) and
 // gemm_fp16_batched (:366-383).  Kernels:
 //
-//  * dma::gemm_f16_dma (f16_dma_gemm.hpp) -- large aligned shapes: 256x256x64
-//    tiles, A staged by LDS DMA, B transposed through VGPRs, three-stage
-//    pipeline, one tile per CU.
+//  * dma::gemm_f16_big (f16_dma_gemm.hpp) -- large aligned shapes: 256x256x64
+//    tiles of v_mfma_f32_16x16x32_f16, A and B staged by LDS DMA, B fragments
+//    from transposing LDS reads, one tile per CU.
 //  * mg::mfma_gemm with the fp16 row loader for A and the transposing fp16
 //    column loader for B (mfma_gemm.hpp): LDS-tiled v_mfma_f32_32x32x16_f16,
 //    tile shape chosen per (M, N), split-K when the tile grid is too small to
@@ -210,7 +210,7 @@ clove_status_t run_mfma(Params p, int batch, int num_cus, hipStream_t stream) {
     return check_launch();
 }
 
-using BigTile = dma::Cfg<256, 256, 64, 2, 2>;
+using BigTile = dma::Big;
 
 // The DMA kernel's preconditions: 16-byte aligned operands, K a multiple of
 // the K tile, N a multiple of 8, every per-batch operand addressable with
@@ -227,7 +227,7 @@ clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int ba
                 cdiv(M, BigTile::BM), cdiv(N, BigTile::BN)};
     const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * batch;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
-    hipLaunchKernelGGL((dma::gemm_f16_dma<BigTile>), dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
+    hipLaunchKernelGGL(dma::gemm_f16_big<dma::Big>, dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
     return check_launch();
 }
 

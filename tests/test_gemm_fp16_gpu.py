@@ -165,9 +165,10 @@ def test_repeat_calls_deterministic_split_k():
 
 # ---- the 256x256x64 DMA-staged kernel (large, aligned shapes) ----
 
-@pytest.mark.parametrize("M,N,K", [(2048, 4096, 512), (3000, 3000, 320), (4096, 2056, 128)])
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 512), (3000, 3000, 320), (4096, 2056, 128), (1536, 2048, 64)])
 def test_big_tile_ragged_edges(M, N, K):
-    # tile grids >= half the CUs with ragged M / N edges (clamped loads)
+    # tile grids >= half the CUs with ragged M / N edges (rows past the end read
+    # as zero, columns past N never stored); K / 64 odd (320) and 1 (64)
     g = rng("big", M, N, K)
     A = g.standard_normal((M, K)).astype(np.float16)
     B = (g.standard_normal((K, N)) * 0.05).astype(np.float16)
