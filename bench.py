@@ -16,7 +16,8 @@ The same JSON line also carries:
   shapes        every other shape of the five named configurations: FP16 512^3
                 and M = 1/32/128 at 4096x4096, INT8 M = 1/128, INT4 W4A4
                 (11008x4096 and 4096x11008, N = 1/16/128), the W4A16 Llama-1B
-                layer at T = 1 and 512; each with t_roof = max(flops / MFMA
+                layer at T = 1 and 512 as the reference runtime sequences it and
+                with gate / up / SwiGLU fused; each with t_roof = max(flops / MFMA
                 peak, bytes / 8 TB/s) and frac_roofline = t_roof / time
 The shapes are timed as HIP-graph replays of one call per operand copy: the
 copies rotate through >= 512 MiB so that no call finds its weights in the
@@ -286,32 +287,61 @@ def extras():
             del Cs, calls
         del sets
 
-    # ---- W4A16 Llama-1B decoder-layer GEMM sequence (QKV, O + residual, gate, up, down + residual) ----
-    layer = [(3072, 2048, 0.0), (2048, 2048, 1.0), (8192, 2048, 0.0), (8192, 2048, 0.0), (2048, 8192, 1.0)]
+    # ---- W4A16 Llama-1B decoder-layer GEMM sequence, as the reference runtime
+    # runs its linear layers (src/runtime/inference.cu:139-194): QKV, O +
+    # residual, gate, up, SwiGLU, down + residual; and the same layer with the
+    # gate / up projections and SwiGLU fused into one pass over a [2I, K/2]
+    # weight (clove_w4a16_swiglu) ----
+    hid, inter = 2048, 8192
+    layer = [(3072, hid, 0.0), (hid, hid, 1.0), (inter, hid, 0.0), (inter, hid, 0.0), (hid, inter, 1.0)]
     wbytes = sum(O * K // 2 + 4 * O * (-(-K // 128)) for O, K, _ in layer)
 
     def make_layer(i):
         return [(u8((O, K // 2), 600 + 10 * i + j), uni16((O, -(-K // 128)), 0.001, 0.02, 700 + 10 * i + j),
                  zeros16((O, -(-K // 128)), 800 + 10 * i + j)) for j, (O, K, _) in enumerate(layer)]
 
+    def fuse_gate_up(L):
+        # [gate rows; up rows] as one weight: the same numbers as L[2], L[3]
+        return [L[0], L[1], tuple(torch.cat([L[2][k], L[3][k]], 0) for k in range(3)), L[4]]
+
     for T in (1, 512):
         layers = [make_layer(i) for i in range(copies_for(wbytes) if T == 1 else 2)]
-        xs = [f16((T, K), 1.0, 900 + j) for j, (O, K, _) in enumerate(layer)]
-        ys = [f16((T, O), 1.0, 950 + j) for j, (O, K, _) in enumerate(layer)]
+        x = f16((T, hid), 1.0, 900)
+        attn = f16((T, hid), 1.0, 901)
+        q = torch.empty(T, 3072, dtype=torch.float16, device="cuda")
+        res = f16((T, hid), 1.0, 902)
+        gate = torch.empty(T, inter, dtype=torch.float16, device="cuda")
+        up = torch.empty_like(gate)
+        h = torch.empty_like(gate)
 
-        def step(L, xs=xs, ys=ys, T=T):
-            for j, (O, K, beta) in enumerate(layer):
-                w, s, z = L[j]
-                cg.gemm_w4a16(xs[j], w, s, z, ys[j], T, O, K, 1.0, beta)
+        def step(L, T=T):
+            cg.gemm_w4a16(x, *L[0], q, T, 3072, hid, 1.0, 0.0)
+            cg.gemm_w4a16(attn, *L[1], res, T, hid, hid, 1.0, 1.0)
+            cg.gemm_w4a16(x, *L[2], gate, T, inter, hid, 1.0, 0.0)
+            cg.gemm_w4a16(x, *L[3], up, T, inter, hid, 1.0, 0.0)
+            cg.swiglu(gate, up, h, T * inter)
+            cg.gemm_w4a16(h, *L[4], res, T, hid, inter, 1.0, 1.0)
 
-        # the residual projections accumulate into ys across calls: compare the
-        # non-residual outputs only
-        calls = [lambda L=L: step(L) for L in layers]
+        def step_fused(L, T=T):
+            cg.gemm_w4a16(x, *L[0], q, T, 3072, hid, 1.0, 0.0)
+            cg.gemm_w4a16(attn, *L[1], res, T, hid, hid, 1.0, 1.0)
+            cg.w4a16_swiglu(x, *L[2], h, T, inter, hid)
+            cg.gemm_w4a16(h, *L[3], res, T, hid, inter, 1.0, 1.0)
+
         flops = sum(2 * T * O * K for O, K, _ in layer)
-        nb = wbytes + sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
-        record(f"w4a16_llama1b_layer_T{T}", calls, [ys[0], ys[2], ys[3]], flops, nb, PEAK_FP16_TFLOPS,
-               replays=5 if T == 1 else 3)
+        lin = sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
+        # the residual projections accumulate into res across calls: compare the
+        # other outputs only
+        calls = [lambda L=L: step(L) for L in layers]
+        record(f"w4a16_llama1b_layer_T{T}", calls, [q, gate, up, h], flops,
+               wbytes + lin + 3 * 2 * T * inter, PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3)
+        fused = [fuse_gate_up(L) for L in layers]
         del layers, calls
+        calls = [lambda L=L: step_fused(L) for L in fused]
+        lin_f = lin - 2 * (2 * T * hid + 2 * T * inter) + (2 * T * hid + 2 * T * inter)
+        record(f"w4a16_llama1b_layer_fused_T{T}", calls, [q, h], flops, wbytes + lin_f,
+               PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3)
+        del fused, calls
     return out
 
 

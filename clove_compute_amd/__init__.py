@@ -17,5 +17,8 @@ from .gemm import (  # noqa: F401
     gemm_int8_rowcol,
     gemm_w4a16,
     release_scratch,
+    swiglu,
+    swiglu_fused,
+    w4a16_swiglu,
 )
 from . import quant  # noqa: F401

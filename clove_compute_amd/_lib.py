@@ -40,6 +40,9 @@ SIGNATURES = {
     "clove_gemm_int4": ([P, P, P, P, P, P, P, I, I, I, P], I),
     "clove_gemm_int4_ex": ([P, P, P, P, P, P, P, I, I, I, I, P], I),
     "clove_gemm_w4a16": ([P, P, P, P, P, I, I, I, F, F, P], I),
+    "clove_swiglu": ([P, P, P, I, P], I),
+    "clove_swiglu_fused": ([P, P, P, P, I, I, I, P], I),
+    "clove_w4a16_swiglu": ([P, P, P, P, P, I, I, I, P], I),
     "clove_release_scratch": ([], I),
 }
 

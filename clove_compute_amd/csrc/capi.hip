@@ -5,6 +5,7 @@
 
 #include <map>
 #include <mutex>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -33,6 +34,18 @@ struct ScratchEntry {
 };
 std::mutex g_scratch_mu;
 std::map<std::pair<int, void*>, ScratchEntry> g_scratch;
+
+// other library buffers per (device, stream, slot)
+struct BufferEntry {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+std::map<std::tuple<int, void*, int>, BufferEntry> g_buffers;  // guarded by g_scratch_mu
+
+__global__ void zero_u16(uint16_t* p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
 
 __global__ void zero_u32(unsigned* p, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -104,6 +117,30 @@ clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t 
     e.view.counters = counters;
     e.view.num_counters = nc;
     *out = e.view;
+    return CLOVE_OK;
+}
+
+clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    BufferEntry& e = g_buffers[std::make_tuple(dev, reinterpret_cast<void*>(stream), slot)];
+    if (e.base && e.bytes >= bytes) {
+        *out = e.base;
+        return CLOVE_OK;
+    }
+    const size_t nb = round_up_pow2(bytes, (size_t)1 << 20);
+    if (e.base) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return CLOVE_ERR_LAUNCH;
+        (void)hipFree(e.base);
+        e = BufferEntry{};
+    }
+    if (hipMalloc(&e.base, nb) != hipSuccess) {
+        e = BufferEntry{};
+        return CLOVE_ERR_OUT_OF_MEMORY;
+    }
+    e.bytes = nb;
+    *out = e.base;
     return CLOVE_OK;
 }
 
@@ -273,6 +310,68 @@ clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q, const void* W
     return launch_w4a16(a, static_cast<hipStream_t>(stream));
 }
 
+static bool same_or_disjoint(const void* a, const void* b, size_t bytes) {
+    return a == b || !overlaps(a, bytes, b, bytes);
+}
+
+clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int size, void* stream) {
+    if (size < 0) return CLOVE_ERR_INVALID_DIM;
+    if (size == 0) return CLOVE_OK;
+    if (!gate || !up || !output) return CLOVE_ERR_NULL_POINTER;
+    if (!aligned2(gate) || !aligned2(up) || !aligned2(output)) return CLOVE_ERR_INVALID_ARG;
+    // elementwise: the output may be one of the inputs, but not shifted against it
+    const size_t b = (size_t)size * 2;
+    if (!same_or_disjoint(output, gate, b) || !same_or_disjoint(output, up, b)) return CLOVE_ERR_ALIASING;
+    return launch_swiglu(static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                         static_cast<uint16_t*>(output), size, static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const void* W_up, void* output,
+                                  int batch_seq, int hidden_dim, int intermediate_dim, void* stream) {
+    const int T = batch_seq, H = hidden_dim, I = intermediate_dim;
+    if (T < 0 || H < 0 || I < 0) return CLOVE_ERR_INVALID_DIM;
+    if (T == 0 || I == 0) return CLOVE_OK;
+    if (!output || (H > 0 && (!input || !W_gate || !W_up))) return CLOVE_ERR_NULL_POINTER;
+    if (!aligned2(input) || !aligned2(W_gate) || !aligned2(W_up) || !aligned2(output))
+        return CLOVE_ERR_INVALID_ARG;
+    const size_t bo = (size_t)T * I * 2;
+    if (overlaps(output, bo, input, (size_t)T * H * 2) || overlaps(output, bo, W_gate, (size_t)H * I * 2) ||
+        overlaps(output, bo, W_up, (size_t)H * I * 2))
+        return CLOVE_ERR_ALIASING;
+    if ((int64_t)cdiv64(T, 32) * (int64_t)cdiv64(I, 128) > 0x3fffffff) return CLOVE_ERR_INVALID_DIM;
+    return launch_swiglu_fused_fp16(static_cast<const uint16_t*>(input), static_cast<const uint16_t*>(W_gate),
+                                    static_cast<const uint16_t*>(W_up), static_cast<uint16_t*>(output), T, H,
+                                    I, static_cast<hipStream_t>(stream));
+}
+
+clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void* W_scale,
+                                  const void* W_zero, void* H, int T, int I, int K, void* stream) {
+    if (T < 0 || I < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (K % 2 != 0) return CLOVE_ERR_INVALID_ARG;
+    if (T == 0 || I == 0) return CLOVE_OK;
+    if (!H || (K > 0 && (!X || !W_q || !W_scale || !W_zero))) return CLOVE_ERR_NULL_POINTER;
+    if (!aligned2(X) || !aligned2(H) || !aligned2(W_scale) || !aligned2(W_zero)) return CLOVE_ERR_INVALID_ARG;
+    if ((int64_t)2 * I > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
+    const int64_t G = cdiv64(K, 128);
+    const size_t bh = (size_t)T * I * 2;
+    if (overlaps(H, bh, X, (size_t)T * K * 2) || overlaps(H, bh, W_q, (size_t)2 * I * (K / 2)) ||
+        overlaps(H, bh, W_scale, (size_t)2 * I * G * 2) || overlaps(H, bh, W_zero, (size_t)2 * I * G * 2))
+        return CLOVE_ERR_ALIASING;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (K == 0) {  // gate = up = 0: swiglu(0, 0) = +0
+        hipLaunchKernelGGL(zero_u16, dim3(256), dim3(256), 0, s, static_cast<uint16_t*>(H), (size_t)T * I);
+        return check_launch();
+    }
+    W4A16Args a;
+    a.X = static_cast<const uint16_t*>(X);
+    a.W = W_q;
+    a.scale = static_cast<const uint16_t*>(W_scale);
+    a.zero = static_cast<const uint16_t*>(W_zero);
+    a.Y = static_cast<uint16_t*>(H);
+    a.T = T; a.O = I; a.K = K;
+    return launch_w4a16_swiglu(a, s);
+}
+
 clove_status_t clove_release_scratch(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
@@ -282,6 +381,14 @@ clove_status_t clove_release_scratch(void) {
         if (it->first.first == dev) {
             (void)hipFree(it->second.base);
             it = g_scratch.erase(it);
+        } else {
+            ++it;
+        }
+    }
+    for (auto it = g_buffers.begin(); it != g_buffers.end();) {
+        if (std::get<0>(it->first) == dev) {
+            (void)hipFree(it->second.base);
+            it = g_buffers.erase(it);
         } else {
             ++it;
         }

@@ -51,6 +51,15 @@ __device__ __forceinline__ unsigned pack2h(float lo, float hi) {
     return static_cast<unsigned>(f2h(lo)) | (static_cast<unsigned>(f2h(hi)) << 16);
 }
 
+// SwiGLU of one fp16 gate / up pair: fp16(silu(g) * u), silu(x) = x / (1 +
+// exp(-x)) in fp32 (src/kernels/activations.cu:9-11, :76-134); expf is the
+// device library's, the division IEEE fp32
+__device__ __forceinline__ uint16_t swiglu_h(uint16_t g, uint16_t u) {
+    const float x = h2f(g);
+    const float s = x / (1.0f + expf(-x));
+    return f2h(s * h2f(u));
+}
+
 // Streaming GEMVs with V weight columns (or token rows): the wide variants
 // (V >= WIDE) and the byte-gathering unaligned ones need more than the 128
 // VGPRs a 1024-thread workgroup leaves, so they run with at most 512 threads

@@ -83,6 +83,26 @@ clove_status_t launch_w4a16(const W4A16Args& args, hipStream_t stream);
 // it launches and stores the launch status in *status.
 bool try_i4w_w4a16(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 bool try_i4w_int4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+// SwiGLU of a fused gate/up INT4 weight: args.W holds 2 args.O rows (gate rows,
+// then up rows, scales / zeros likewise), args.Y receives H [T, O]
+bool try_i4w_w4a16_swiglu(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+
+// H [T, O] = swiglu(X @ gate^T, X @ up^T) on a fused gate/up W4A16 weight
+// (w4a16.hip): GEMV for T <= 4, the INT4-weight MFMA GEMM above, or, for shapes
+// neither covers, the two linear layers and the elementwise SwiGLU
+clove_status_t launch_w4a16_swiglu(const W4A16Args& args, hipStream_t stream);
+// out[i] = swiglu(gate[i], up[i]), n elements (swiglu.hip)
+clove_status_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
+                             hipStream_t stream);
+// out [T, inter] = swiglu(X @ W_gate, X @ W_up), FP16 weights [hidden, inter]
+clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up,
+                                        uint16_t* out, int T, int hidden, int inter, hipStream_t stream);
+
+// A device buffer of at least `bytes` owned by the library per (device,
+// stream, slot), kept across calls (capi.hip); slot 0 is reserved for the
+// split-K scratch.  Synchronises the stream when it has to grow.
+clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void** out);
+constexpr int kBufSwiglu = 1;  // gate / up intermediates of the unfused SwiGLU paths
 
 // MFMA path for few rows of A against a large N-contiguous B (skinny_gemm.hip):
 // FP16 (any alpha/beta, batched) and INT8 with zero points 0.  Same contract

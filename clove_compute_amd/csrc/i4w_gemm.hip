@@ -41,7 +41,8 @@ Plan make_plan(int R, int C, int G, int cus, int target, int min_groups) {
 template <class CF, bool XS, int OUT, class Prep>
 clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_bytes, hipStream_t stream,
                    Prep prep) {
-    const Plan pl = make_plan<CF>(a.R, a.C, a.G, cus, target, min_groups);
+    // OUT 2 (SwiGLU): a tile of BR weight rows makes BR/2 outputs
+    const Plan pl = make_plan<CF>(OUT == 2 ? 2 * a.R : a.R, a.C, a.G, cus, target, min_groups);
     a.tiles_r = pl.tiles_r;
     a.tiles_c = pl.tiles_c;
     a.nsplit = pl.nsplit;
@@ -80,8 +81,11 @@ clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_byt
 // Splits keep at least 10 (64 x 32) or 8 groups each.
 template <bool XS, int OUT, class Prep>
 clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t stream, Prep prep) {
+    const int rows = OUT == 2 ? 2 * a.R : a.R;  // weight rows
     if (a.C <= 32) return run<CfgC32, XS, OUT>(a, cus, 3 * cus, 10, extra_bytes, stream, prep);
-    if (cdiv(a.R, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= cus)
+    // (SwiGLU tiles pair gate and up rows: the same outputs take twice the
+    // weight rows, so the big tile waits for twice the grid)
+    if (cdiv(rows, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= (OUT == 2 ? 2 : 1) * cus)
         return run<CfgBig, XS, OUT>(a, cus, cus, 8, extra_bytes, stream, prep);
     return run<CfgC64, XS, OUT>(a, cus, 2 * cus, 8, extra_bytes, stream, prep);
 }
@@ -106,6 +110,25 @@ bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status
     a.alpha = w.alpha;
     a.beta = w.beta;
     *status = by_shape<false, 1>(a, cus, 0, stream, [](Args&, char*) { return CLOVE_OK; });
+    return true;
+}
+
+bool try_i4w_w4a16_swiglu(const W4A16Args& w, int cus, hipStream_t stream, clove_status_t* status) {
+    if (w.T <= 4 || w.K <= 0 || w.K % 128 != 0 || !aligned16(w.X) || !aligned16(w.W)) return false;
+    if (!fits31((int64_t)w.T * w.K * 2) || !fits31((int64_t)2 * w.O * (w.K / 2))) return false;
+    Args a{};
+    a.W = w.W;
+    a.wscale = w.scale;
+    a.wzero = w.zero;
+    a.X = w.X;
+    a.out = w.Y;
+    a.R = w.O;  // outputs; the weight has 2 O rows (gate, then up)
+    a.C = w.T;
+    a.K = w.K;
+    a.G = w.K / 128;
+    a.alpha = 1.0f;
+    a.beta = 0.0f;
+    *status = by_shape<false, 2>(a, cus, 0, stream, [](Args&, char*) { return CLOVE_OK; });
     return true;
 }
 

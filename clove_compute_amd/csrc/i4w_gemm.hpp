@@ -63,8 +63,8 @@ struct Args {
     const uint16_t* wzero;   // [R, G] fp16
     const uint16_t* X;       // [C, K] fp16 (rows >= C read as zero)
     const float* xs;         // [G, ldxs] fp32 or null
-    uint16_t* out;           // OUT 0: [R, C] (C[m, n]),  OUT 1: [C, R] (Y[t, o])
-    int R, C, K, G, ldxs;
+    uint16_t* out;           // OUT 0: [R, C] (C[m, n]),  OUT 1 / 2: [C, R] (Y[t, o] / H[t, o])
+    int R, C, K, G, ldxs;    // OUT 2: R output rows, the weight has 2 R (gate, then up)
     float alpha, beta;       // OUT 1 epilogue: alpha * acc + beta * out
     int tiles_r, tiles_c, nsplit, gps;  // gps: groups per split
     float* part;
@@ -166,19 +166,29 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     const int split = bid % p.nsplit;
     const int tile = bid / p.nsplit;
     const int tc = tile % p.tiles_c, tr = tile / p.tiles_c;
-    const int r0 = tr * BR, c0 = tc * BC;
+    // OUT 2 (SwiGLU): in every 32-row block of the tile, rows 0..15 are the
+    // gate rows of 16 outputs and rows 16..31 the up rows (weight rows R + o)
+    // of the same outputs, so each pair meets in lanes l and l ^ 16 of a wave
+    constexpr int HB = OUT == 2 ? BR / 2 : BR;  // output rows per tile
+    const int r0 = tr * HB, c0 = tc * BC;
     const int gbeg = split * p.gps;
     constexpr int KS = CF::KS, SPG = CF::SPG;
     const int nkt = (min(p.G, gbeg + p.gps) - gbeg) * SPG;  // stages of this split
     const int R = p.R, K = p.K, G = p.G;
+    const int RW = OUT == 2 ? 2 * R : R;  // weight rows
+    // weight row of tile row rt (clamped: rows past the end are never stored)
+    auto src_row = [&](int rt) {
+        if constexpr (OUT == 2) return ((rt & 16) ? R : 0) + min(r0 + 16 * (rt >> 5) + (rt & 15), R - 1);
+        else return min(r0 + rt, R - 1);
+    };
 
     const unsigned lds0 = __builtin_amdgcn_readfirstlane(
         (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char*)smem));
 
     // ---- DMA descriptors and per-lane offsets (fixed over K) ----
     const u32x4 rx = make_rsrc(p.X, (unsigned)p.C * K * 2);
-    const u32x4 rw = make_rsrc(p.W, (unsigned)R * (K / 2));
-    const unsigned sz_bytes = ((unsigned)R * G * 2 + 3u) & ~3u;  // see the scale DMA below
+    const u32x4 rw = make_rsrc(p.W, (unsigned)RW * (K / 2));
+    const unsigned sz_bytes = ((unsigned)RW * G * 2 + 3u) & ~3u;  // see the scale DMA below
     const u32x4 rs = make_rsrc(p.wscale, sz_bytes);
     const u32x4 rz = make_rsrc(p.wzero, sz_bytes);
     int offx[CF::DX], offw[CF::DW];
@@ -192,7 +202,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     for (int i = 0; i < CF::DW; ++i) {
         constexpr int CPR = CF::WRB / 16;  // chunks per weight row
         const int row = (1024 / CF::WRB) * (wave * CF::DW + i) + lane / CPR;
-        offw[i] = (r0 + row) * (K / 2) + 16 * ((lane % CPR) ^ swz_w<KS>(row));
+        offw[i] = src_row(row) * (K / 2) + 16 * ((lane % CPR) ^ swz_w<KS>(row));
     }
     // scale / zero: instruction j (of 2 BR / 64) covers rows 64 (j % (BR/64)) + lane,
     // scale for j < BR/64, zero otherwise.  Each lane fetches the aligned dword that
@@ -202,7 +212,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
 #pragma unroll
     for (int i = 0; i < CF::DS; ++i) {
         const int j = wave * CF::DS + i;
-        srow[i] = min(r0 + 64 * (j % (BR / 64)) + lane, R - 1);
+        srow[i] = src_row(64 * (j % (BR / 64)) + lane);
     }
     u32x4 rxs = {0u, 0u, 0u, 0u};
     if constexpr (XS) rxs = make_rsrc(p.xs, (unsigned)G * p.ldxs * 4);
@@ -244,7 +254,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     for (int e = 0; e < NWC; ++e) woff[e] = OFF_W + wrow0 * CF::WRB + 16 * ((NWC * h + e) ^ swz_w<KS>(wrow0));
     int wrow[FW];
 #pragma unroll
-    for (int i = 0; i < FW; ++i) wrow[i] = min(r0 + wrow0 + 32 * i, R - 1);
+    for (int i = 0; i < FW; ++i) wrow[i] = src_row(wrow0 + 32 * i);
 
     f32x16 acc[FW][FX];
 #pragma unroll
@@ -385,6 +395,31 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     }
 
     // ---- epilogue ----
+    if constexpr (OUT == 2) {
+        // lane l (l % 32 < 16) holds gate, lane l ^ 16 up, for output row o and
+        // the same tokens.  v_permlane16_swap on the accumulators of two tokens
+        // (x: token e, y: token e + 1) leaves gate(e) and up(e) in lane l and
+        // gate(e + 1) and up(e + 1) in lane l ^ 16: both lanes finish one output.
+        const bool up_lane = (l32 & 16) != 0;
+#pragma unroll
+        for (int i = 0; i < FW; ++i) {
+            const int r = r0 + 16 * (wr * FW + i) + (l32 & 15);
+#pragma unroll
+            for (int j = 0; j < FX; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        const auto sw = __builtin_amdgcn_permlane16_swap(bitcast<unsigned>(acc[i][j][4 * q + e]),
+                                                                         bitcast<unsigned>(acc[i][j][4 * q + e + 1]),
+                                                                         false, false);
+                        const int c = c0 + wc * 32 * FX + 32 * j + 8 * q + 4 * h + e + (up_lane ? 1 : 0);
+                        if (r < R && c < p.C)
+                            p.out[(int64_t)c * R + r] = swiglu_h(f2h(bitcast<float>(sw[0])), f2h(bitcast<float>(sw[1])));
+                    }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
         const int r = r0 + wrow0 + 32 * i;

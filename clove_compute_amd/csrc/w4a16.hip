@@ -10,9 +10,16 @@
 //    with 16-byte loads, all in flight at once; the nibbles are turned into the
 //    exact fp16 integers q - z and dotted with X (staged in LDS) by
 //    v_dot2_f32_f16 in fp32; acc += scale * that per 32-k chunk.
-//  * larger T -- the shared MFMA GEMM (mfma_gemm.hpp): X rows as operand A,
-//    W rows unpacked to the exact integers q - z as operand B; the per-group
-//    fp32 partials are scaled by s[o,g] after each 128-wide group.
+//  * larger T -- the INT4-weight MFMA GEMM (i4w_gemm.hpp) when K % 128 == 0
+//    and the operands are aligned, else the shared MFMA GEMM (mfma_gemm.hpp):
+//    X rows as operand A, W rows unpacked to the exact integers q - z as
+//    operand B; the per-group fp32 partials are scaled by s[o,g] after each
+//    128-wide group.
+//
+// launch_w4a16_swiglu: the MLP's gate and up projections and SwiGLU in one
+// pass over a fused [2 O, K/2] weight (gate rows, then up rows): the GEMV and
+// the MFMA GEMM pair each gate row with its up row inside a workgroup, so
+// neither projection is written to memory.
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "mfma_gemm.hpp"
@@ -48,8 +55,15 @@ __host__ __device__ constexpr int xperm(int k) { return (k & ~7) | ((k & 1) << 2
 // the fp16 values 1024 + q (v_perm against 0x64 bytes), minus 1024 + z gives
 // q - z exactly, and v_dot2_f32_f16 with the X pairs accumulates
 // sum_k x_k (q_k - z) in fp32 with exact products; acc += s * that per chunk.
-template <int TV, int RPW, int UPR, bool ALIGNED>
+//
+// SWIGLU: the weight holds 2 O rows (gate rows 0..O-1, then up rows O..2O-1)
+// and the output is H [T, O] = swiglu(fp16(gate), fp16(up)); a wave takes RPW/2
+// gate rows and the RPW/2 up rows of the same outputs, so the pair meets in
+// one lane's registers.
+template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false>
 __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_gemv(GemvParams p) {
+    static_assert(!SWIGLU || RPW % 2 == 0, "gate / up row pairs");
+    constexpr int LR = SWIGLU ? RPW / 2 : RPW;  // output rows per wave
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
     const int NT = blockDim.x, WPB = NT >> 6;  // waves per workgroup (rows / RPW)
     constexpr int XPT = 4;  // X prefetch: 16-byte pieces per thread
@@ -57,10 +71,11 @@ __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_ge
     const int nch = p.nch, K = p.K, G = p.G, KP = 32 * nch;
     uint16_t* Xs = reinterpret_cast<uint16_t*>(lds);
 
-    const int row0 = (blockIdx.x * WPB + wave) * RPW;
-    int ridx[RPW];  // rows past O read the last row and are not stored
+    const int row0 = (blockIdx.x * WPB + wave) * LR;  // first output row of the wave
+    int ridx[RPW];  // weight rows; rows past O read the last row and are not stored
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) ridx[r] = min(row0 + r, p.O - 1);
+    for (int r = 0; r < RPW; ++r)
+        ridx[r] = (SWIGLU && r >= LR) ? p.O + min(row0 + r - LR, p.O - 1) : min(row0 + r % LR, p.O - 1);
 
     // ---- X: 16-byte pieces (8 k) into registers first ----
     const int npieces = TV * KP / 8;
@@ -149,7 +164,7 @@ __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_ge
             const int cs = min(c, nch - 1);  // lanes past the end: garbage, masked by s = 0
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
-                const bool valid = row0 + r < p.O && c < nch;
+                const bool valid = row0 + r % LR < p.O && c < nch;
                 const float sc = valid ? h2f(sh[r][u]) : 0.0f;
                 const f16x2 zz = mg::magic_zero(zh[r][u]);
                 f16x2 qz[16];
@@ -186,6 +201,22 @@ __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_ge
 #pragma unroll
             for (int t = 0; t < TV; ++t) acc[r][t] += __shfl_xor(acc[r][t], off);
     // lane t (t < T) writes token t of every row
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int r = 0; r < LR; ++r) {
+            const int row = row0 + r;
+            if (row >= p.O || lane >= p.T || lane >= TV) continue;
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int t = 0; t < TV; ++t)
+                if (t == lane) {
+                    g = acc[r][t];
+                    u = acc[r + LR][t];
+                }
+            p.Y[(int64_t)lane * p.O + row] = swiglu_h(f2h(g), f2h(u));
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
@@ -224,18 +255,28 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     return g;
 }
 
-template <int TV, int RPW, int UPR>
+template <int TV, int RPW, int UPR, bool SWIGLU = false>
 clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(TV, p.nch);
     wpb = min(wpb, (aligned ? gemv_max_threads<TV, true, 2>() : gemv_max_threads<TV, false, 2>()) / 64);
-    const dim3 grid(cdiv(p.O, wpb * RPW));
-    auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true> : w4a16_gemv<TV, RPW, UPR, false>;
+    const dim3 grid(cdiv(p.O, wpb * (SWIGLU ? RPW / 2 : RPW)));
+    auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true, SWIGLU> : w4a16_gemv<TV, RPW, UPR, false, SWIGLU>;
     if (lds > 64 * 1024 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
     hipLaunchKernelGGL(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
+}
+
+// SwiGLU: gate / up pairs, so at least two weight rows per wave (the shape
+// is chosen for the 2 O weight rows)
+template <int TV>
+clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    const GemvShape g = gemv_shape(2 * p.O, p.nch, cus);
+    if (g.rpw <= 2) return run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return run_gemv_shape<TV, 4, 2, true>(p, g.wpb, aligned, stream);
+    return run_gemv_shape<TV, 8, 1, true>(p, g.wpb, aligned, stream);
 }
 
 template <int TV>
@@ -281,6 +322,39 @@ clove_status_t run_mfma(mg::Params p, int cus, hipStream_t stream) {
 
 }  // namespace
 }  // namespace w4
+
+clove_status_t launch_w4a16_swiglu(const W4A16Args& a, hipStream_t stream) {
+    using namespace w4;
+    DeviceInfo dev;
+    clove_status_t st = current_device_info(&dev);
+    if (st != CLOVE_OK) return st;
+    const int G = cdiv(a.K, 128);
+    const int nch = cdiv(a.K, 32);
+    const int tv = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
+    if (a.T <= 4 && gemv_lds_bytes(tv, nch) <= kMaxGemvLds) {
+        GemvParams p{a.X, a.W, a.scale, a.zero, a.Y, a.T, a.O, a.K, G, nch, 1.0f, 0.0f};
+        const bool aligned = aligned16(a.W) && (a.K % 32 == 0);
+        if (tv == 1) return run_gemv_swiglu<1>(p, aligned, dev.num_cus, stream);
+        if (tv == 2) return run_gemv_swiglu<2>(p, aligned, dev.num_cus, stream);
+        return run_gemv_swiglu<4>(p, aligned, dev.num_cus, stream);
+    }
+    clove_status_t st2;
+    if (try_i4w_w4a16_swiglu(a, dev.num_cus, stream, &st2)) return st2;
+    // other shapes: gate into H, up into a library buffer, SwiGLU in place
+    void* ubuf = nullptr;
+    st = acquire_buffer(stream, kBufSwiglu, (size_t)a.T * a.O * 2, &ubuf);
+    if (st != CLOVE_OK) return st;
+    W4A16Args g = a, u = a;
+    g.alpha = u.alpha = 1.0f;
+    g.beta = u.beta = 0.0f;
+    u.W = a.W + (size_t)a.O * (a.K / 2);
+    u.scale = a.scale + (size_t)a.O * G;
+    u.zero = a.zero + (size_t)a.O * G;
+    u.Y = static_cast<uint16_t*>(ubuf);
+    if ((st = launch_w4a16(g, stream)) != CLOVE_OK) return st;
+    if ((st = launch_w4a16(u, stream)) != CLOVE_OK) return st;
+    return launch_swiglu(a.Y, u.Y, a.Y, (int64_t)a.T * a.O, stream);
+}
 
 clove_status_t launch_w4a16(const W4A16Args& a, hipStream_t stream) {
     using namespace w4;

@@ -97,5 +97,28 @@ def gemm_w4a16(X, W_q, W_scale, W_zero, Y, T: int, O: int, K: int, alpha: float 
                "gemm_w4a16")
 
 
+def swiglu(gate, up, output, size: int, stream=None) -> None:
+    """output = fp16(silu(gate) * up) elementwise (include/clove/kernels/activations.cuh:25-31);
+    output may be gate or up."""
+    _lib.check(_lib.lib().clove_swiglu(_ptr(gate), _ptr(up), _ptr(output), size, _stream(stream)),
+               "swiglu")
+
+
+def swiglu_fused(input, W_gate, W_up, output, batch_seq: int, hidden_dim: int,
+                 intermediate_dim: int, stream=None) -> None:
+    """output = swiglu(input @ W_gate, input @ W_up) on FP16 weights [hidden, intermediate]
+    (declared in include/clove/kernels/activations.cuh:37-46)."""
+    _lib.check(_lib.lib().clove_swiglu_fused(_ptr(input), _ptr(W_gate), _ptr(W_up), _ptr(output),
+                                             batch_seq, hidden_dim, intermediate_dim,
+                                             _stream(stream)), "swiglu_fused")
+
+
+def w4a16_swiglu(X, W_q, W_scale, W_zero, H, T: int, I: int, K: int, stream=None) -> None:
+    """H = swiglu(X @ dequant(W[:I])^T, X @ dequant(W[I:2I])^T): the MLP's gate and up
+    projections and SwiGLU on one fused INT4 weight [2I, K/2] (gate rows first)."""
+    _lib.check(_lib.lib().clove_w4a16_swiglu(_ptr(X), _ptr(W_q), _ptr(W_scale), _ptr(W_zero),
+                                             _ptr(H), T, I, K, _stream(stream)), "w4a16_swiglu")
+
+
 def release_scratch() -> None:
     _lib.check(_lib.lib().clove_release_scratch(), "release_scratch")

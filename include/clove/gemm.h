@@ -66,6 +66,21 @@ inline void gemm_fp16_batched(const half* A, const half* B, half* C, int batch, 
         clove_gemm_fp16_batched(A, B, C, batch, M, N, K, alpha, beta, stream));
 }
 
+// include/clove/kernels/activations.cuh:25-31
+inline void swiglu(const half* gate, const half* up, half* output, int size,
+                   hipStream_t stream = 0) {
+    CLOVE_CHECK_STATUS(clove_swiglu(gate, up, output, size, stream));
+}
+
+// include/clove/kernels/activations.cuh:37-46 (declared, never defined, in the
+// reference)
+inline void swiglu_fused(const half* input, const half* W_gate, const half* W_up, half* output,
+                         int batch_seq, int hidden_dim, int intermediate_dim,
+                         hipStream_t stream = 0) {
+    CLOVE_CHECK_STATUS(clove_swiglu_fused(input, W_gate, W_up, output, batch_seq, hidden_dim,
+                                          intermediate_dim, stream));
+}
+
 // Extensions (no reference counterpart; see <clove/gemm_c.h>).
 inline void gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q, const half* A_scale,
                              const half* B_scale, half* C, int M, int N, int K,
@@ -86,6 +101,12 @@ inline void gemm_w4a16(const half* X, const uint8_t* W_q, const half* W_scale,
                        float beta = 0.0f, hipStream_t stream = 0) {
     CLOVE_CHECK_STATUS(
         clove_gemm_w4a16(X, W_q, W_scale, W_zero, Y, T, O, K, alpha, beta, stream));
+}
+
+inline void w4a16_swiglu(const half* X, const uint8_t* W_q, const half* W_scale,
+                         const half* W_zero, half* H, int T, int I, int K,
+                         hipStream_t stream = 0) {
+    CLOVE_CHECK_STATUS(clove_w4a16_swiglu(X, W_q, W_scale, W_zero, H, T, I, K, stream));
 }
 
 }  // namespace clove

@@ -153,8 +153,46 @@ clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q,
                                 int T, int O, int K, float alpha, float beta,
                                 void* stream);
 
-/* Frees the scratch buffers held for the current device (all streams).
- * Synchronises the device first.  No reference counterpart. */
+/*
+ * SwiGLU: output[i] = fp16(silu(gate[i]) * up[i]), silu(x) = x / (1 + exp(-x))
+ * in fp32.  Replaces clove::swiglu (include/clove/kernels/activations.cuh:25-31,
+ * src/kernels/activations.cu:76-134).  `output` may be `gate` or `up` (in place).
+ */
+clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int size,
+                            void* stream);
+
+/*
+ * Fused gate/up projections and SwiGLU on FP16 weights:
+ *   output[t,i] = swiglu(fp16(input @ W_gate)[t,i], fp16(input @ W_up)[t,i])
+ * input [batch_seq, hidden_dim], W_gate / W_up [hidden_dim, intermediate_dim]
+ * (gemm_fp16's B layout), output [batch_seq, intermediate_dim], all fp16.
+ * Replaces clove::swiglu_fused, declared in include/clove/kernels/
+ * activations.cuh:37-46 and never defined there.  Runs the two FP16 GEMMs
+ * (the up projection into a library-owned buffer per stream, kept like the
+ * split-K scratch) and the SwiGLU pass.
+ */
+clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const void* W_up,
+                                  void* output, int batch_seq, int hidden_dim,
+                                  int intermediate_dim, void* stream);
+
+/*
+ * Fused MLP gate/up projections and SwiGLU on group-128 INT4 weights:
+ *   H[t,i] = swiglu(gate[t,i], up[t,i]),
+ *   gate = fp16(X @ dequant(W[0:I])^T),  up = fp16(X @ dequant(W[I:2I])^T)
+ * X [T,K] fp16; W_q [2I, K/2] in gemm_int4's A layout with the I gate rows
+ * first and the I up rows after them; W_scale / W_zero [2I, K/128] fp16;
+ * H [T,I] fp16.  K even.  The reference MLP's gate and up gemm_fp16 calls and
+ * its swiglu (src/runtime/inference.cu:172-186) in one pass that writes
+ * neither projection to memory (when K % 128 == 0 and X, W_q are 16-byte
+ * aligned, or T <= 4; other shapes run the two W4A16 layers and SwiGLU).
+ */
+clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void* W_scale,
+                                  const void* W_zero, void* H, int T, int I, int K,
+                                  void* stream);
+
+/* Frees the scratch buffers held for the current device (all streams),
+ * including the SwiGLU intermediates.  Synchronises the device first.  No
+ * reference counterpart. */
 clove_status_t clove_release_scratch(void);
 
 #ifdef __cplusplus

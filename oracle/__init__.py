@@ -54,6 +54,7 @@ def lib():
             "oracle_gemm_int4_literal": ([P, P, P, P, P, I, I, I], None),
             "oracle_gemm_int4_groupwise": ([P, P, P, P, P, P, P, P, P, I, I, I], None),
             "oracle_w4a16": ([P, P, P, P, P, P, P, I, I, I, D, D], None),
+            "oracle_swiglu": ([P, P, P, I64], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -194,3 +195,29 @@ def w4a16(X, W_q, W_scale, W_zero, Y_in=None, alpha=1.0, beta=0.0):
     lib().oracle_w4a16(_p(X), _p(W_q), _p(W_scale), _p(W_zero), _p(Yin), _p(Y),
                        _p(out64), T, O, K, alpha, beta)
     return Y, out64
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """The reference's SwiGLU (src/kernels/activations.cu:9-11, :76-134) on fp16
+    gate / up of equal shape: fp16(silu(g) * u), silu in fp32."""
+    g = _c(gate, np.float16)
+    u = _c(up, np.float16)
+    if g.shape != u.shape:
+        raise ValueError("gate and up must have the same shape")
+    out = np.empty(g.shape, np.float16)
+    lib().oracle_swiglu(_p(g), _p(u), _p(out), g.size)
+    return out
+
+
+def w4a16_swiglu(X, W_q, W_scale, W_zero) -> np.ndarray:
+    """H [T, I] = swiglu(gate, up), gate = fp16(X @ dequant(W[:I])^T), up likewise on
+    W[I:2I]: the reference MLP's gate / up linear layers and SwiGLU
+    (src/runtime/inference.cu:172-186) on one fused INT4 weight [2I, K/2] whose
+    first I rows are the gate projection and the next I rows the up projection."""
+    W_q = _c(W_q, np.uint8)
+    I = W_q.shape[0] // 2
+    if W_q.shape[0] != 2 * I:
+        raise ValueError("the fused gate/up weight needs an even number of rows")
+    gate, _ = w4a16(X, W_q[:I], W_scale[:I], W_zero[:I])
+    up, _ = w4a16(X, W_q[I:], W_scale[I:], W_zero[I:])
+    return swiglu(gate, up)

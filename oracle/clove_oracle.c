@@ -379,3 +379,18 @@ void oracle_w4a16(const uint16_t* X, const uint8_t* W_q, const uint16_t* W_scale
     free(w);
     free(x);
 }
+
+/*
+ * SwiGLU on fp16 gate / up (src/kernels/activations.cu:9-11 silu_f,
+ * :76-134 swiglu_kernel): out = fp16(silu(g) * u), g and u widened exactly
+ * to fp32, silu(x) = x / (1 + expf(-x)) in fp32, the product rounded to fp32
+ * and then to fp16 (__float2half of a float).
+ */
+void oracle_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        const float x = oracle_f16_to_f32(gate[i]);
+        const float s = x / (1.0f + expf(-x));
+        const float r = s * oracle_f16_to_f32(up[i]);
+        out[i] = oracle_f32_to_f16(r);
+    }
+}

@@ -103,6 +103,10 @@ void oracle_w4a16(const uint16_t* X, const uint8_t* W_q, const uint16_t* W_scale
                   const uint16_t* W_zero, const uint16_t* Y_in, uint16_t* Y,
                   double* out64, int T, int O, int K, double alpha, double beta);
 
+/* out[i] = fp16(silu(f32(gate[i])) * f32(up[i])), silu(x) = x / (1 + expf(-x))
+ * in fp32 (src/kernels/activations.cu:9-11, :76-134). */
+void oracle_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,3 +115,24 @@ def test_w4a16_validation(L):
     assert f(A, W, None, Z, C, 4, 4, 8, 1.0, 0.0, None) == _lib.CLOVE_ERR_NULL_POINTER
     assert f(A, W, S, Z, W, 4, 4, 8, 1.0, 0.0, None) == _lib.CLOVE_ERR_ALIASING
     assert f(A, W, S, Z, C, 0, 4, 8, 1.0, 0.0, None) == _lib.CLOVE_OK
+
+
+def test_swiglu_validation(L):
+    f = L.clove_swiglu
+    assert f(A, B, C, -1, None) == _lib.CLOVE_ERR_INVALID_DIM
+    assert f(A, B, C, 0, None) == _lib.CLOVE_OK
+    assert f(None, B, C, 8, None) == _lib.CLOVE_ERR_NULL_POINTER
+    assert f(A + 1, B, C, 8, None) == _lib.CLOVE_ERR_INVALID_ARG
+    assert f(A, B, A + 2, 8, None) == _lib.CLOVE_ERR_ALIASING  # shifted against an input
+    g = L.clove_swiglu_fused
+    assert g(A, B, B, C, 4, -1, 8, None) == _lib.CLOVE_ERR_INVALID_DIM
+    assert g(A, B, B, C, 0, 4, 8, None) == _lib.CLOVE_OK
+    assert g(A, None, B, C, 4, 4, 8, None) == _lib.CLOVE_ERR_NULL_POINTER
+    assert g(A, B, B, B, 4, 4, 8, None) == _lib.CLOVE_ERR_ALIASING
+    W, S, Z = 0x400000, 0x500000, 0x600000
+    h = L.clove_w4a16_swiglu
+    assert h(A, W, S, Z, C, 4, 4, 9, None) == _lib.CLOVE_ERR_INVALID_ARG
+    assert h(A, W, S, Z, C, 4, -4, 8, None) == _lib.CLOVE_ERR_INVALID_DIM
+    assert h(A, W, S, None, C, 4, 4, 8, None) == _lib.CLOVE_ERR_NULL_POINTER
+    assert h(A, W, S, Z, Z, 4, 4, 8, None) == _lib.CLOVE_ERR_ALIASING
+    assert h(A, W, S, Z, C, 4, 0, 8, None) == _lib.CLOVE_OK

@@ -295,3 +295,63 @@ def test_w4a16_against_float64_dequant():
     Y, out64 = oracle.w4a16(X, pack_rows(q), s, z, Yin, alpha=1.0, beta=1.0)
     assert np.allclose(out64, ref, rtol=1e-12, atol=1e-12)
     assert np.array_equal(f16bits(Y), f16bits(out64.astype(np.float32).astype(np.float16)))
+
+
+# ---- SwiGLU (src/kernels/activations.cu:9-11 silu_f, :76-134 swiglu_kernel) ----
+
+def _swiglu_f64(g, u):
+    """fp16(silu(g) * u) with silu and the product in float64, then one rounding
+    to fp16 through fp32 (differs from the fp32 restatement only at rounding ties)"""
+    g64 = g.astype(np.float64)
+    s = g64 / (1.0 + np.exp(-g64))
+    return (s * u.astype(np.float64)).astype(np.float32).astype(np.float16)
+
+
+def test_swiglu_closed_forms():
+    g = np.array([0.0, -0.0, 1.0, -1.0, 2.0, 20.0, -20.0, 65504.0, -65504.0], np.float16)
+    u = np.ones_like(g)
+    out = oracle.swiglu(g, u).astype(np.float64)
+    # silu(0) = 0, silu(x) -> x for x >> 0, silu(x) -> 0- for x << 0,
+    # silu(1) = 1 / (1 + 1/e), silu(-1) = -1 / (1 + e)
+    assert out[0] == 0.0 and out[1] == 0.0
+    assert abs(out[2] - 1.0 / (1.0 + np.exp(-1.0))) < 1e-3
+    assert abs(out[3] + 1.0 / (1.0 + np.e)) < 1e-3
+    assert abs(out[4] - 2.0 / (1.0 + np.exp(-2.0))) < 2e-3
+    assert out[5] == 20.0 and out[7] == 65504.0
+    assert -1e-7 < out[6] < 0.0 and out[8] == 0.0  # exp(65504) overflows: -65504 / inf = -0
+    # linear in up
+    g2 = RNG.standard_normal(64).astype(np.float16)
+    one = oracle.swiglu(g2, np.ones_like(g2))
+    assert np.array_equal(f16bits(oracle.swiglu(g2, np.full_like(g2, 2.0))),
+                          f16bits((one.astype(np.float32) * 2).astype(np.float16)))
+
+
+def test_swiglu_against_float64_formula():
+    n = 1 << 16
+    g = (RNG.standard_normal(n) * 4).astype(np.float16)
+    u = (RNG.standard_normal(n) * 2).astype(np.float16)
+    out = oracle.swiglu(g, u)
+    ref = _swiglu_f64(g, u)
+    d = np.abs(f16bits(out).astype(np.int32) - f16bits(ref).astype(np.int32))
+    # fp32 intermediates: at most one fp16 ulp, and only at rounding boundaries
+    assert d.max() <= 1 and np.count_nonzero(d) < n // 1000
+    # a restatement with the sign of the exponent flipped is caught
+    bad = (g.astype(np.float64) / (1.0 + np.exp(g.astype(np.float64))) * u).astype(np.float16)
+    assert np.count_nonzero(f16bits(bad) != f16bits(out)) > n // 2
+
+
+def test_w4a16_swiglu_is_gate_up_then_swiglu():
+    T, I, K = 3, 24, 256
+    G = K // 128
+    X = RNG.standard_normal((T, K)).astype(np.float16)
+    q = RNG.integers(0, 16, (2 * I, K))
+    s = RNG.uniform(0.001, 0.02, (2 * I, G)).astype(np.float16)
+    z = RNG.integers(0, 16, (2 * I, G)).astype(np.float16)
+    H = oracle.w4a16_swiglu(X, pack_rows(q), s, z)
+    W = (q - np.repeat(z.astype(np.float64), 128, axis=1)) * np.repeat(s.astype(np.float64), 128, axis=1)
+    lin = X.astype(np.float64) @ W.T
+    gate = lin[:, :I].astype(np.float32).astype(np.float16)
+    up = lin[:, I:].astype(np.float32).astype(np.float16)
+    assert H.shape == (T, I)
+    d = np.abs(f16bits(H).astype(np.int32) - f16bits(_swiglu_f64(gate, up)).astype(np.int32))
+    assert d.max() <= 1
