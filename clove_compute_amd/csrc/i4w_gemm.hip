@@ -2,6 +2,7 @@
 // split-K plan, scratch, and the B transpose of group-wise INT4.
 #include "dispatch.hpp"
 #include "i4w_gemm.hpp"
+#include "i4w_stream.hpp"
 
 namespace clove {
 namespace {
@@ -92,6 +93,41 @@ clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t 
 
 bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 
+// ---- the streaming kernel (i4w_stream.hpp) for C <= 32 X rows ----
+template <int WF, int XF, int NG, int KS, bool XS, int OUT>
+clove_status_t launch_stream(const Args& a, hipStream_t stream) {
+    using SC = SCfg<WF, XF, NG, KS>;
+    const int lds = SC::lds_bytes(a.G, XS);
+    hipLaunchKernelGGL((i4w_stream<SC, XS, OUT>), dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream,
+                       a);
+    return check_launch();
+}
+
+// K slices: the fewest waves (2, 4 or 8) that leave each at most 11 groups,
+// unrolled for 8 groups when that suffices
+template <int WF, int XF, bool XS, int OUT>
+clove_status_t stream_by_k(const Args& a, hipStream_t stream) {
+    const int G = a.G;
+    if (G <= 16) return launch_stream<WF, XF, 8, 2, XS, OUT>(a, stream);
+    if (G <= 22) return launch_stream<WF, XF, 11, 2, XS, OUT>(a, stream);
+    if (G <= 32) return launch_stream<WF, XF, 8, 4, XS, OUT>(a, stream);
+    if (G <= 44) return launch_stream<WF, XF, 11, 4, XS, OUT>(a, stream);
+    if (G <= 64) return launch_stream<WF, XF, 8, 8, XS, OUT>(a, stream);
+    return launch_stream<WF, XF, 11, 8, XS, OUT>(a, stream);
+}
+
+constexpr int kStreamMaxGroups = 88;  // K <= 11264
+
+// Two weight fragments (32 rows) per workgroup when that still gives every
+// CU a workgroup, else one (measured on the 11008 x 4096 and 4096 x 11008
+// shapes: 32 rows and 4 slices, 16 rows and 8 slices)
+template <bool XS, int OUT>
+clove_status_t run_stream(const Args& a, int cus, hipStream_t stream) {
+    const bool wf2 = cdiv(a.R, 32) >= cus;
+    if (a.C <= 16) return wf2 ? stream_by_k<2, 1, XS, OUT>(a, stream) : stream_by_k<1, 1, XS, OUT>(a, stream);
+    return wf2 ? stream_by_k<2, 2, XS, OUT>(a, stream) : stream_by_k<1, 2, XS, OUT>(a, stream);
+}
+
 }  // namespace
 
 bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status_t* status) {
@@ -109,6 +145,10 @@ bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status
     a.G = w.K / 128;
     a.alpha = w.alpha;
     a.beta = w.beta;
+    if (w.T <= 32 && a.G <= kStreamMaxGroups) {
+        *status = run_stream<false, 1>(a, cus, stream);
+        return true;
+    }
     *status = by_shape<false, 1>(a, cus, 0, stream, [](Args&, char*) { return CLOVE_OK; });
     return true;
 }
@@ -162,6 +202,15 @@ bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t
         args.xs = xs;
         return check_launch();
     };
+    if (q.N <= 16 && G <= kStreamMaxGroups) {
+        // the B transpose into scratch, then the streaming kernel
+        Scratch s;
+        clove_status_t st = acquire_scratch(stream, xt_bytes + xs_bytes, 0, &s);
+        if (st == CLOVE_OK) st = prep(a, reinterpret_cast<char*>(s.partials));
+        if (st == CLOVE_OK) st = run_stream<true, 0>(a, cus, stream);
+        *status = st;
+        return true;
+    }
     *status = by_shape<true, 0>(a, cus, xt_bytes + xs_bytes, stream, prep);
     return true;
 }

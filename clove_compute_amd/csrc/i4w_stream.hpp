@@ -1,0 +1,267 @@
+// Streaming MFMA GEMM with packed INT4 weight rows for few X rows (C <= 32):
+// group-wise INT4 with N in 9..32 columns and W4A16 with 5..32 tokens.  The
+// same arithmetic as i4w_gemm (i4w_gemm.hpp):
+//
+//   out[r, c] = sum_g  sw[r,g] * sx[g,c] * P_g[r,c]
+//   P_g[r,c]  = sum_{k in group g} (q[r,k] - zw[r,g]) * x[c,k]        (exact)
+//
+// shaped for the weight stream: no LDS stages and no barriers in the K loop.
+// A workgroup of KS waves owns 16 WF weight rows; wave w takes groups
+// [w gq, (w+1) gq) of K and loads its rows' 64-byte group slices straight into
+// VGPRs, D groups ahead of the one it computes, so that the whole weight
+// matrix is in flight across the grid at once.  X (shared by every workgroup,
+// served by L2) is loaded the same way.  The workgroup's scales, zero points
+// (and sx) are copied to LDS once at the start; the KS partial sums of an
+// output meet in LDS once at the end, in wave order.
+//
+// One v_mfma_f32_16x16x32_f16 per (16 X rows, 16 weight rows, 32 k): the X
+// fragment is the "A" operand (lane l: X row l % 16) and the weight fragment
+// the "B" operand (lane l: weight row l % 16), so each lane owns one weight
+// row and four X rows of the result.  In step q of a group, lane group
+// h = l / 16 holds k = 32 q + 8 h .. + 7, so that the four lane groups of one
+// X load read 64 contiguous bytes of a row.  A weight row's group slice
+// arrives as one 16-byte load per lane (lane group h: k = 32 h .. 32 h + 31,
+// dword j = k 32 h + 8 j) and a 4 x 4 transpose across lane groups and
+// dwords (v_permlane16_swap, then v_permlane32_swap) gives lane group h the
+// dwords of k = 32 q + 8 h.
+#pragma once
+
+#include "i4w_gemm.hpp"
+
+namespace clove {
+namespace i4w {
+
+// WF: 16-row weight fragments per wave, XF: 16-row X fragments (C <= 16 XF),
+// NG: groups per wave (gq <= NG), KS: waves (K slices) per workgroup,
+// D: groups in flight ahead of the computed one
+template <int WF_, int XF_, int NG_, int KS_, int D_ = 4>
+struct SCfg {
+    static constexpr int WF = WF_, XF = XF_, NG = NG_, KS = KS_, D = D_ < NG_ ? D_ : NG_;
+    static constexpr int NT = 64 * KS, ROWS = 16 * WF;
+    // partial sums of the KS waves, then the workgroup's scales and zero
+    // points ([ROWS][G] fp16 each) and sx ([G][16 XF] fp32)
+    static constexpr int RED_BYTES = KS * XF * WF * 4 * 64 * 4;
+    static constexpr int lds_bytes(int G, bool xs) {
+        return RED_BYTES + 2 * ((ROWS * G * 2 + 15) & ~15) + (xs ? G * 16 * XF * 4 : 0);
+    }
+};
+
+// lane group h of (r0, r1, r2, r3) holds dwords 4 h .. 4 h + 3 of a 16-dword
+// block; afterwards register q holds dword 4 q + h
+__device__ __forceinline__ u32x4 transpose_lane_groups(u32x4 v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(v.x, v.y, false, false);
+    const auto b = __builtin_amdgcn_permlane16_swap(v.z, v.w, false, false);
+    const auto c = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+    return u32x4{c[0], d[0], c[1], d[1]};
+}
+
+template <class SC, bool XS, int OUT>
+__global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
+    constexpr int WF = SC::WF, XF = SC::XF, NG = SC::NG, D = SC::D, ROWS = SC::ROWS;
+    extern __shared__ __attribute__((aligned(16))) float red[];
+
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 4, l16 = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int R = p.R, K = p.K, G = p.G;
+    const int r0 = blockIdx.x * ROWS;
+    const int gq = (G + SC::KS - 1) / SC::KS;
+    const int g0 = wave * gq, g1 = min(G, g0 + gq);  // this wave's groups (none when g0 >= G)
+    uint16_t* lds_s = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(red) + SC::RED_BYTES);
+    uint16_t* lds_z = lds_s + ((ROWS * G + 7) & ~7);
+    float* lds_xs = reinterpret_cast<float*>(lds_z + ((ROWS * G + 7) & ~7));
+
+    const uint8_t* wrow[WF];
+#pragma unroll
+    for (int f = 0; f < WF; ++f)  // rows past R read the last row and are never stored
+        wrow[f] = p.W + (int64_t)min(r0 + 16 * f + l16, R - 1) * (K / 2) + 16 * h;
+    const uint16_t* xrow[XF];
+#pragma unroll
+    for (int j = 0; j < XF; ++j) xrow[j] = p.X + (int64_t)min(16 * j + l16, p.C - 1) * K + 8 * h;
+
+    struct Slot {
+        u32x4 w[WF];
+        f16x8 x[XF][4];
+    };
+    Slot slot[D];
+    auto issue = [&](Slot& s, int j) {
+        const int g = max(0, min(g0 + j, g1 - 1));
+#pragma unroll
+        for (int f = 0; f < WF; ++f)
+            s.w[f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[f] + 64 * g));
+#pragma unroll
+        for (int x = 0; x < XF; ++x)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s.x[x][q] = *reinterpret_cast<const f16x8*>(xrow[x] + 128 * g + 32 * q);
+    };
+
+    // ---- the workgroup's scales, zero points and sx to LDS; their loads go
+    // out first, so that waiting for them does not wait for the weight stream
+    // issued right behind ----
+    constexpr int SPT = 8;  // staged elements per thread per pass
+    const int nsz = ROWS * G;
+    const int nxs = XS ? G * 16 * XF : 0;
+    uint16_t sv[SPT], zv[SPT];
+    float xv[SPT] = {};
+    // unconditional loads from clamped addresses (a guarded load becomes a
+    // branch whose merge waits for it, and for everything issued before it)
+    auto stage_load = [&](int base) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int idx = base + i * SC::NT + tid;
+            const int is = min(idx, nsz - 1);
+            const int64_t src = (int64_t)min(r0 + is / G, R - 1) * G + is % G;
+            sv[i] = p.wscale[src];
+            zv[i] = p.wzero[src];
+            if constexpr (XS) {
+                const int e = min(max(idx - nsz, 0), nxs - 1), g = e / (16 * XF), c = e % (16 * XF);
+                xv[i] = p.xs[(int64_t)g * p.ldxs + c];
+            }
+        }
+    };
+    auto stage_store = [&](int base) {
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int idx = base + i * SC::NT + tid;
+            if (idx < nsz) {
+                lds_s[idx] = sv[i];
+                lds_z[idx] = zv[i];
+            } else if (XS && idx < nsz + nxs) {
+                lds_xs[idx - nsz] = xv[i];
+            }
+        }
+    };
+    stage_load(0);
+    __builtin_amdgcn_sched_barrier(0);  // (keep the order: staging loads, then the stream)
+#pragma unroll
+    for (int j = 0; j < D; ++j) issue(slot[j], j);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_store(0);
+    // (more than SPT elements per thread: rare, and those loads wait behind the stream)
+    for (int base = SPT * SC::NT; base < nsz + nxs; base += SPT * SC::NT) {
+        stage_load(base);
+        stage_store(base);
+    }
+    __syncthreads();
+
+    f32x4 acc[XF][WF];
+#pragma unroll
+    for (int j = 0; j < XF; ++j)
+#pragma unroll
+        for (int f = 0; f < WF; ++f) acc[j][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    {
+        // groups past g1 reload the last one (an L2 hit; a wave without groups
+        // reloads group G - 1) and fold with scale 0: straight-line code, so
+        // every wait the compiler places is for one slot
+        auto compute = [&](const Slot& s, int j) {
+            const int g = max(0, min(g0 + j, g1 - 1));
+            const bool valid = g0 + j < g1;
+            f32x4 P[XF][WF];
+            u32x4 wt[WF];
+            f16x2 zz[WF];
+#pragma unroll
+            for (int f = 0; f < WF; ++f) {
+                wt[f] = transpose_lane_groups(s.w[f]);
+                const _Float16 nz = (_Float16)(-rintf(h2f(lds_z[(16 * f + l16) * G + g])) * (1.0f / 512.0f));
+                zz[f] = f16x2{nz, nz};
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int f = 0; f < WF; ++f) {
+                    const unsigned wd = q == 0 ? wt[f].x : q == 1 ? wt[f].y : q == 2 ? wt[f].z : wt[f].w;
+                    const f16x8 wf = unpack8(wd, zz[f]);
+#pragma unroll
+                    for (int x = 0; x < XF; ++x)
+                        P[x][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            s.x[x][q], wf, q == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : P[x][f], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < WF; ++f) {
+                // (q - z) 2^-9 back to q - z; 0 for the reloaded tail groups
+                const float wsc = valid ? h2f(lds_s[(16 * f + l16) * G + g]) * 512.0f : 0.0f;
+#pragma unroll
+                for (int x = 0; x < XF; ++x) {
+                    f32x4 sc = {wsc, wsc, wsc, wsc};
+                    if constexpr (XS) {
+                        const f32x4 sx = *reinterpret_cast<const f32x4*>(lds_xs + g * 16 * XF + 16 * x + 4 * h);
+                        sc = sc * sx;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[x][f][e] = fmaf(sc[e], P[x][f][e], acc[x][f][e]);
+                }
+            }
+        };
+        // sched_barrier: keep the loads where they are written (the scheduler
+        // would sink them toward their use to save registers, which shortens
+        // the prefetch to nothing)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            compute(slot[j % D], j);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j + D < NG) issue(slot[j % D], j + D);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- the KS partials of each output, summed in wave order ----
+    constexpr int NV = XF * WF * 4;
+    if constexpr (SC::KS > 1) {
+#pragma unroll
+        for (int x = 0; x < XF; ++x)
+#pragma unroll
+            for (int f = 0; f < WF; ++f)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[((wave * NV) + (x * WF + f) * 4 + e) * 64 + lane] = acc[x][f][e];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int x = 0; x < XF; ++x)
+#pragma unroll
+            for (int f = 0; f < WF; ++f)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = acc[x][f][e];
+                    for (int w = 1; w < SC::KS; ++w) v += red[((w * NV) + (x * WF + f) * 4 + e) * 64 + lane];
+                    acc[x][f][e] = v;
+                }
+    }
+
+    // ---- epilogue: lane holds weight row r0 + 16 f + l16 and X rows 16 x + 4 h .. + 3 ----
+#pragma unroll
+    for (int f = 0; f < WF; ++f) {
+        const int r = r0 + 16 * f + l16;
+        if (r >= R) continue;
+#pragma unroll
+        for (int x = 0; x < XF; ++x) {
+            const int c = 16 * x + 4 * h;
+            if constexpr (OUT == 0) {
+                uint16_t* dst = p.out + (int64_t)r * p.C + c;
+                if (c + 3 < p.C && (p.C & 3) == 0) {
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(acc[x][f][0], acc[x][f][1]),
+                                                           pack2h(acc[x][f][2], acc[x][f][3])};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c + e < p.C) dst[e] = f2h(acc[x][f][e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (c + e < p.C) {
+                        uint16_t* dst = p.out + (int64_t)(c + e) * R + r;
+                        float v = p.alpha * acc[x][f][e];
+                        if (p.beta != 0.0f) v = fmaf(p.beta, h2f(*dst), v);
+                        *dst = f2h(v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace i4w
+}  // namespace clove

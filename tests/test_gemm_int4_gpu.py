@@ -148,3 +148,23 @@ def test_groupwise_mfma_path_pow2_bit_exact(M, N, K):
     rows = np.arange(M) if M <= 1000 else np.unique(np.concatenate([[0, M - 1], g.integers(0, M, 32)]))
     _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
     assert np.array_equal(f16bits(C[rows]), f16bits(ref.astype(np.float16)))
+
+
+# group-wise, 9..16 columns, K % 128 == 0: the B transpose, then the
+# streaming kernel (i4w_stream.hpp): K slices of 2, 4 and 8 waves (G = 1, 20,
+# 40, 86), ragged M (fewer rows than one fragment), odd N
+@pytest.mark.parametrize("M,N,K", [(7, 9, 128), (300, 12, 2560), (1000, 16, 5120), (33, 15, 11008)])
+def test_groupwise_stream_path(M, N, K):
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "stream")
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    ok, rep = within_tol(C, ref)
+    assert ok, rep
+
+
+def test_groupwise_stream_path_pow2_bit_exact():
+    M, N, K = 520, 16, 4096
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2st", pow2=True, small=True)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))

@@ -100,3 +100,27 @@ def test_mfma_path_pow2_bit_exact(T, O, K):
     Y = run(X, W, s, z, None, O)
     _, ref = oracle.w4a16(X, W, s, z)
     assert np.array_equal(f16bits(Y), f16bits(ref.astype(np.float16)))
+
+
+# 5..32 tokens with K % 128 == 0 take the streaming kernel (i4w_stream.hpp):
+# every K-slice configuration (G = 1, 10, 20, 30, 40, 60, 86 groups: 2, 4 or 8
+# waves of up to 8 or 11 groups, waves without groups when G is small), one
+# and two 16-token fragments, one and two 16-row weight fragments per
+# workgroup (8192 rows), ragged weight rows, alpha/beta
+@pytest.mark.parametrize("T,O,K", [(5, 77, 128), (16, 300, 1280), (17, 130, 2560), (32, 1000, 3840),
+                                   (8, 8192, 5120), (31, 8192, 7680), (12, 4096, 11008 // 128 * 128)])
+def test_stream_path_shapes(T, O, K):
+    X, W, s, z, g = make(T, O, K, "stream")
+    Yin = g.standard_normal((T, O)).astype(np.float16)
+    Y = run(X, W, s, z, Yin, O, 0.75, 0.5)
+    _, ref = oracle.w4a16(X, W, s, z, Yin, 0.75, 0.5)
+    ok, rep = within_tol(Y, ref)
+    assert ok, rep
+
+
+@pytest.mark.parametrize("T,O,K", [(6, 200, 1024), (32, 96, 11008 // 128 * 128)])
+def test_stream_path_pow2_bit_exact(T, O, K):
+    X, W, s, z, _ = make(T, O, K, "pow2s", pow2=True)
+    Y = run(X, W, s, z, None, O)
+    _, ref = oracle.w4a16(X, W, s, z)
+    assert np.array_equal(f16bits(Y), f16bits(ref.astype(np.float16)))
