@@ -161,8 +161,12 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave % CF::WR, wc = wave / CF::WR;
 
-    // ---- tile, split, K range ----
-    const int bid = blockIdx.x;
+    // ---- tile, split, K range.  Workgroups are dealt to the 8 XCDs round
+    // robin (workgroup b runs on XCD b % 8) and each XCD has its own L2, so
+    // the grid is renumbered to give every XCD a contiguous run of (tile,
+    // split) pairs: the splits of a tile and the X-row tiles of a weight-row
+    // tile then share one L2 (measured: split-K shapes 3-12 % faster) ----
+    const int bid = gridDim.x % 8 == 0 ? (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8) : (int)blockIdx.x;
     const int split = bid % p.nsplit;
     const int tile = bid / p.nsplit;
     const int tc = tile % p.tiles_c, tr = tile / p.tiles_c;
