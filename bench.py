@@ -190,6 +190,27 @@ def cpu_baseline(h, seconds):
                 parity_rows_ok=bool(ok))
 
 
+def device_info():
+    """Compute units and the maximum shader clock the runtime reports (the
+    peaks above assume 256 CUs at 2.4 GHz; under sustained MFMA load the clock
+    runs lower, which is why the measured fraction of peak is a clock-bound
+    figure, not a per-cycle one)."""
+    import ctypes
+
+    import torch
+    props = torch.cuda.get_device_properties(0)
+    info = {"name": props.name, "arch": getattr(props, "gcnArchName", None), "cus": props.multi_processor_count}
+    try:
+        hip = ctypes.CDLL("libamdhip64.so")
+        v = ctypes.c_int(0)
+        # hipDeviceAttributeClockRate (kHz)
+        if hip.hipDeviceGetAttribute(ctypes.byref(v), 5, 0) == 0 and v.value > 0:
+            info["max_sclk_mhz"] = v.value // 1000
+    except OSError:
+        pass
+    return info
+
+
 def copies_for(nbytes):
     return max(2, -(-ROTATE_BYTES // max(1, nbytes)))
 
@@ -239,6 +260,7 @@ def extras():
         if hot_calls is not None:
             d["us_hot"] = graph_time(hot_calls, outputs[:1], replays)
         out[name] = d
+        print(f"[bench] {name}: {us:.2f} us", file=sys.stderr, flush=True)
 
     # ---- FP16: 512^3 (U[-1,1]) and the decode/prefill rows of the LLM shapes ----
     A5, B5 = u16((512, 512), 1), u16((512, 512), 2)
@@ -361,6 +383,7 @@ def main():
 
     timer = Timer()
     h = headline(args, timer)
+    print(f"[bench] headline: {h['ms'] * 1e3:.1f} us per call", file=sys.stderr, flush=True)
     flops = 2.0 * 4096 ** 3
     achieved = h["tflops"]
     traffic = None
@@ -383,6 +406,7 @@ def main():
         "data": "synthetic (seeded numpy PCG64: A ~ N(0,1), B ~ N(0,0.02), fp16)",
         "config": {"workload": "fp16_gemm_4096x4096x4096", "M": 4096, "N": 4096, "K": 4096,
                    "layout": "row-major A[M,K] B[K,N] C[M,N]", "accumulate": "fp32"},
+        "device": device_info(),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic, "flops_per_launch": flops,
