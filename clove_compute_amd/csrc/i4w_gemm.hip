@@ -94,26 +94,30 @@ clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t 
 bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 
 // ---- the streaming kernel (i4w_stream.hpp) for C <= 32 X rows ----
-template <int WF, int XF, int NG, int KS, bool XS, int OUT>
+template <int WF, int XF, int NG, int KS, bool XS, int OUT, bool RAWB>
 clove_status_t launch_stream(const Args& a, hipStream_t stream) {
     using SC = SCfg<WF, XF, NG, KS>;
-    const int lds = SC::lds_bytes(a.G, XS);
-    hipLaunchKernelGGL((i4w_stream<SC, XS, OUT>), dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream,
-                       a);
+    const int lds = SC::lds_bytes(a.G, XS, RAWB);
+    auto k = i4w_stream<SC, XS, OUT, RAWB>;
+    if (lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
+            hipSuccess)
+        return CLOVE_ERR_LAUNCH;
+    hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream, a);
     return check_launch();
 }
 
 // K slices: the fewest waves (2, 4 or 8) that leave each at most 11 groups,
 // unrolled for 8 groups when that suffices
-template <int WF, int XF, bool XS, int OUT>
+template <int WF, int XF, bool XS, int OUT, bool RAWB = false>
 clove_status_t stream_by_k(const Args& a, hipStream_t stream) {
     const int G = a.G;
-    if (G <= 16) return launch_stream<WF, XF, 8, 2, XS, OUT>(a, stream);
-    if (G <= 22) return launch_stream<WF, XF, 11, 2, XS, OUT>(a, stream);
-    if (G <= 32) return launch_stream<WF, XF, 8, 4, XS, OUT>(a, stream);
-    if (G <= 44) return launch_stream<WF, XF, 11, 4, XS, OUT>(a, stream);
-    if (G <= 64) return launch_stream<WF, XF, 8, 8, XS, OUT>(a, stream);
-    return launch_stream<WF, XF, 11, 8, XS, OUT>(a, stream);
+    if (G <= 16) return launch_stream<WF, XF, 8, 2, XS, OUT, RAWB>(a, stream);
+    if (G <= 22) return launch_stream<WF, XF, 11, 2, XS, OUT, RAWB>(a, stream);
+    if (G <= 32) return launch_stream<WF, XF, 8, 4, XS, OUT, RAWB>(a, stream);
+    if (G <= 44) return launch_stream<WF, XF, 11, 4, XS, OUT, RAWB>(a, stream);
+    if (G <= 64) return launch_stream<WF, XF, 8, 8, XS, OUT, RAWB>(a, stream);
+    return launch_stream<WF, XF, 11, 8, XS, OUT, RAWB>(a, stream);
 }
 
 constexpr int kStreamMaxGroups = 88;  // K <= 11264
@@ -172,7 +176,10 @@ bool try_i4w_w4a16_swiglu(const W4A16Args& w, int cus, hipStream_t stream, clove
     return true;
 }
 
+bool try_i4w_int4_rawb(const Int4Args& q, int cus, hipStream_t stream, clove_status_t* status);
+
 bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t* status) {
+    if (try_i4w_int4_rawb(q, cus, stream, status)) return true;
     if (q.mode != CLOVE_INT4_GROUPWISE || q.N <= 8 || q.K <= 0 || q.K % 128 != 0 || !aligned16(q.A))
         return false;
     const int Npad = (q.N + 63) / 64 * 64;
@@ -212,6 +219,32 @@ bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t
         return true;
     }
     *status = by_shape<true, 0>(a, cus, xt_bytes + xs_bytes, stream, prep);
+    return true;
+}
+
+bool try_i4w_int4_rawb(const Int4Args& q, int cus, hipStream_t stream, clove_status_t* status) {
+    // 15 or 16 columns: B rows are 8 bytes, read in place (no transpose pass)
+    const int G = q.K / 128;
+    if (q.mode != CLOVE_INT4_GROUPWISE || (q.N != 15 && q.N != 16) || q.K <= 0 || q.K % 128 != 0 ||
+        G > kStreamMaxGroups || !aligned16(q.A) || !aligned16(q.B) || !fits31((int64_t)q.M * (q.K / 2)))
+        return false;
+    Args a{};
+    a.W = q.A;
+    a.wscale = q.A_scale;
+    a.wzero = q.A_zero;
+    a.out = q.C;
+    a.R = q.M;
+    a.C = q.N;
+    a.K = q.K;
+    a.G = G;
+    a.B = q.B;
+    a.bscale = q.B_scale;
+    a.bzero = q.B_zero;
+    a.N = q.N;
+    a.alpha = 1.0f;
+    a.beta = 0.0f;
+    *status = cdiv(a.R, 32) >= cus ? stream_by_k<2, 1, true, 0, true>(a, stream)
+                                   : stream_by_k<1, 1, true, 0, true>(a, stream);
     return true;
 }
 

@@ -69,6 +69,12 @@ struct Args {
     int tiles_r, tiles_c, nsplit, gps;  // gps: groups per split
     float* part;
     unsigned* counters;
+    // raw group-wise INT4 B for the streaming kernel's fused transpose
+    // (i4w_stream.hpp): B [K, 8] bytes (N = 15 or 16), sB / zB [G, N] fp16
+    const uint8_t* B;
+    const uint16_t* bscale;
+    const uint16_t* bzero;
+    int N;
 };
 
 // KS: 16-wide k-steps per stage, 8 (a whole 128-k group) or 4 (half a group:

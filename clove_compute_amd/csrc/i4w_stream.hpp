@@ -24,6 +24,14 @@
 // dword j = k 32 h + 8 j) and a 4 x 4 transpose across lane groups and
 // dwords (v_permlane16_swap, then v_permlane32_swap) gives lane group h the
 // dwords of k = 32 q + 8 h.
+//
+// RAWB (group-wise INT4 with 15 or 16 columns): no transpose pre-pass.  B
+// [K, 8] bytes (16 nibbles per k row) is contiguous, so each wave copies the
+// 1 KB of every group it owns into LDS by LDS DMA at the start, and in step q
+// a lane gathers the nibble of its column from the 8 rows of k = 32 q + 8 h
+// (two distinct dwords per 16-lane group: broadcast reads), packs them in the
+// weights' nibble order and unpacks them with the same exact (q - z) 2^-9
+// arithmetic; the extra 2^-9 is returned in the fold.
 #pragma once
 
 #include "i4w_gemm.hpp"
@@ -41,8 +49,9 @@ struct SCfg {
     // partial sums of the KS waves, then the workgroup's scales and zero
     // points ([ROWS][G] fp16 each) and sx ([G][16 XF] fp32)
     static constexpr int RED_BYTES = KS * XF * WF * 4 * 64 * 4;
-    static constexpr int lds_bytes(int G, bool xs) {
-        return RED_BYTES + 2 * ((ROWS * G * 2 + 15) & ~15) + (xs ? G * 16 * XF * 4 : 0);
+    static constexpr int lds_bytes(int G, bool xs, bool rawb = false) {
+        return RED_BYTES + 2 * ((ROWS * G * 2 + 15) & ~15) + (xs ? G * 16 * XF * 4 : 0) +
+               (rawb ? ((G * 16 * 2 + 15) & ~15) + G * 1024 : 0);
     }
 };
 
@@ -56,9 +65,10 @@ __device__ __forceinline__ u32x4 transpose_lane_groups(u32x4 v) {
     return u32x4{c[0], d[0], c[1], d[1]};
 }
 
-template <class SC, bool XS, int OUT>
+template <class SC, bool XS, int OUT, bool RAWB = false>
 __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     constexpr int WF = SC::WF, XF = SC::XF, NG = SC::NG, D = SC::D, ROWS = SC::ROWS;
+    static_assert(!RAWB || (XS && XF == 1), "raw B: group-wise INT4, 16 columns");
     extern __shared__ __attribute__((aligned(16))) float red[];
 
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 4, l16 = lane & 15;
@@ -70,6 +80,8 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     uint16_t* lds_s = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(red) + SC::RED_BYTES);
     uint16_t* lds_z = lds_s + ((ROWS * G + 7) & ~7);
     float* lds_xs = reinterpret_cast<float*>(lds_z + ((ROWS * G + 7) & ~7));
+    uint16_t* lds_zb = reinterpret_cast<uint16_t*>(lds_xs + (XS ? G * 16 * XF : 0));  // RAWB: zB [G][16]
+    unsigned char* lds_b = reinterpret_cast<unsigned char*>(lds_zb) + ((G * 16 * 2 + 15) & ~15);  // RAWB: B
 
     const uint8_t* wrow[WF];
 #pragma unroll
@@ -77,7 +89,22 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
         wrow[f] = p.W + (int64_t)min(r0 + 16 * f + l16, R - 1) * (K / 2) + 16 * h;
     const uint16_t* xrow[XF];
 #pragma unroll
-    for (int j = 0; j < XF; ++j) xrow[j] = p.X + (int64_t)min(16 * j + l16, p.C - 1) * K + 8 * h;
+    for (int j = 0; j < XF; ++j)
+        xrow[j] = RAWB ? nullptr : p.X + (int64_t)min(16 * j + l16, p.C - 1) * K + 8 * h;
+
+    if constexpr (RAWB) {
+        // this wave's groups of B (1 KB each: 128 k rows x 8 bytes) to LDS,
+        // ahead of every other load so that the first wait for those covers them
+        const u32x4 rb = dma::make_rsrc(p.B, (unsigned)K * 8);
+        const unsigned lb = __builtin_amdgcn_readfirstlane(
+            (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char*)lds_b));
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const int g = max(0, min(g0 + j, g1 - 1));
+            dma::dma16(rb, lb + (unsigned)g * 1024u, 16 * lane, g * 1024);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     struct Slot {
         u32x4 w[WF];
@@ -89,10 +116,13 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
 #pragma unroll
         for (int f = 0; f < WF; ++f)
             s.w[f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[f] + 64 * g));
+        if constexpr (!RAWB) {
 #pragma unroll
-        for (int x = 0; x < XF; ++x)
+            for (int x = 0; x < XF; ++x)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) s.x[x][q] = *reinterpret_cast<const f16x8*>(xrow[x] + 128 * g + 32 * q);
+                for (int q = 0; q < 4; ++q)
+                    s.x[x][q] = *reinterpret_cast<const f16x8*>(xrow[x] + 128 * g + 32 * q);
+        }
     };
 
     // ---- the workgroup's scales, zero points and sx to LDS; their loads go
@@ -101,7 +131,7 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     constexpr int SPT = 8;  // staged elements per thread per pass
     const int nsz = ROWS * G;
     const int nxs = XS ? G * 16 * XF : 0;
-    uint16_t sv[SPT], zv[SPT];
+    uint16_t sv[SPT], zv[SPT], sbv[SPT] = {}, zbv[SPT] = {};
     float xv[SPT] = {};
     // unconditional loads from clamped addresses (a guarded load becomes a
     // branch whose merge waits for it, and for everything issued before it)
@@ -113,7 +143,14 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
             const int64_t src = (int64_t)min(r0 + is / G, R - 1) * G + is % G;
             sv[i] = p.wscale[src];
             zv[i] = p.wzero[src];
-            if constexpr (XS) {
+            if constexpr (RAWB) {
+                // sB and zB (converted, and zeroed past N, at the store: a
+                // use here would wait for the load before the stream goes out)
+                const int e = min(max(idx - nsz, 0), nxs - 1), g = e / 16, c = e % 16;
+                const int64_t si = (int64_t)g * p.N + min(c, p.N - 1);
+                sbv[i] = p.bscale[si];
+                zbv[i] = p.bzero[si];
+            } else if constexpr (XS) {
                 const int e = min(max(idx - nsz, 0), nxs - 1), g = e / (16 * XF), c = e % (16 * XF);
                 xv[i] = p.xs[(int64_t)g * p.ldxs + c];
             }
@@ -127,7 +164,13 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
                 lds_s[idx] = sv[i];
                 lds_z[idx] = zv[i];
             } else if (XS && idx < nsz + nxs) {
-                lds_xs[idx - nsz] = xv[i];
+                if constexpr (RAWB) {
+                    const bool in = (idx - nsz) % 16 < p.N;
+                    lds_xs[idx - nsz] = in ? h2f(sbv[i]) : 0.0f;
+                    lds_zb[idx - nsz] = in ? zbv[i] : (uint16_t)0;
+                } else {
+                    lds_xs[idx - nsz] = xv[i];
+                }
             }
         }
     };
@@ -166,8 +209,33 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
                 const _Float16 nz = (_Float16)(-rintf(h2f(lds_z[(16 * f + l16) * G + g])) * (1.0f / 512.0f));
                 zz[f] = f16x2{nz, nz};
             }
+            f16x2 zzb;
+            unsigned bshift = 0;
+            const unsigned char* brow = nullptr;
+            if constexpr (RAWB) {
+                const _Float16 nzb = (_Float16)(-rintf(h2f(lds_zb[g * 16 + l16])) * (1.0f / 512.0f));
+                zzb = f16x2{nzb, nzb};
+                // column l16: byte l16 / 2 of a row, the high nibble for even columns
+                bshift = 8 * ((l16 >> 1) & 3) + ((l16 & 1) ? 0 : 4);
+                brow = lds_b + (g * 128 + 8 * h) * 8 + 4 * (l16 >> 3);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                f16x8 xq[XF];
+                if constexpr (RAWB) {
+                    // rows k = 128 g + 32 q + 8 h + r, r < 8, packed as the weights
+                    // are: byte j holds row 2j in the high nibble, 2j + 1 in the low
+                    unsigned wx = 0;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const unsigned d = *reinterpret_cast<const unsigned*>(brow + (32 * q + r) * 8);
+                        wx |= ((d >> bshift) & 15u) << (8 * (r >> 1) + ((r & 1) ? 0 : 4));
+                    }
+                    xq[0] = unpack8(wx, zzb);
+                } else {
+#pragma unroll
+                    for (int x = 0; x < XF; ++x) xq[x] = s.x[x][q];
+                }
 #pragma unroll
                 for (int f = 0; f < WF; ++f) {
                     const unsigned wd = q == 0 ? wt[f].x : q == 1 ? wt[f].y : q == 2 ? wt[f].z : wt[f].w;
@@ -175,13 +243,13 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
 #pragma unroll
                     for (int x = 0; x < XF; ++x)
                         P[x][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            s.x[x][q], wf, q == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : P[x][f], 0, 0, 0);
+                            xq[x], wf, q == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : P[x][f], 0, 0, 0);
                 }
             }
 #pragma unroll
             for (int f = 0; f < WF; ++f) {
                 // (q - z) 2^-9 back to q - z; 0 for the reloaded tail groups
-                const float wsc = valid ? h2f(lds_s[(16 * f + l16) * G + g]) * 512.0f : 0.0f;
+                const float wsc = valid ? h2f(lds_s[(16 * f + l16) * G + g]) * (RAWB ? 262144.0f : 512.0f) : 0.0f;
 #pragma unroll
                 for (int x = 0; x < XF; ++x) {
                     f32x4 sc = {wsc, wsc, wsc, wsc};

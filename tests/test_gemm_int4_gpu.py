@@ -150,10 +150,13 @@ def test_groupwise_mfma_path_pow2_bit_exact(M, N, K):
     assert np.array_equal(f16bits(C[rows]), f16bits(ref.astype(np.float16)))
 
 
-# group-wise, 9..16 columns, K % 128 == 0: the B transpose, then the
-# streaming kernel (i4w_stream.hpp): K slices of 2, 4 and 8 waves (G = 1, 20,
-# 40, 86), ragged M (fewer rows than one fragment), odd N
-@pytest.mark.parametrize("M,N,K", [(7, 9, 128), (300, 12, 2560), (1000, 16, 5120), (33, 15, 11008)])
+# group-wise, 9..16 columns, K % 128 == 0: the streaming kernel
+# (i4w_stream.hpp), after the B transpose for N < 15 and reading B in place
+# for N = 15, 16: K slices of 2, 4 and 8 waves (G = 1, 2, 20, 40, 86), ragged
+# M (fewer rows than one fragment), odd N (N = 15: the pad nibble of each B
+# row is read and its column dropped)
+@pytest.mark.parametrize("M,N,K", [(7, 9, 128), (5, 16, 128), (40, 16, 256), (300, 12, 2560), (1000, 16, 5120),
+                                   (33, 15, 11008)])
 def test_groupwise_stream_path(M, N, K):
     A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "stream")
     C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
