@@ -487,33 +487,49 @@ __global__ void __launch_bounds__(256) i4w_prep_b(const uint8_t* __restrict__ B,
     const int b0 = 64 * blockIdx.y;     // first byte column of the tile (column n = 2 b0)
     const bool dw = (ldb & 3) == 0 && (reinterpret_cast<uintptr_t>(B) & 3) == 0;
     // this thread's output columns n0 .. n0 + 7 and k rows 8 k8 .. + 7; their
-    // zero points (and, for k8 == 0, scales) are loaded together with the tile
-    // so that the workgroup makes one round trip to memory
+    // zero points and scales are loaded together with the tile so that the
+    // workgroup makes one round trip to memory.  Every load is unconditional,
+    // from a clamped address, and masked afterwards: a guarded load becomes a
+    // branch whose merge waits for it, which would serialize the round trips.
     const int c8 = tid & 15, k8 = tid >> 4;
     const int n0 = 2 * b0 + 8 * c8;
     uint16_t zh[8], sh16[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-        const int n = n0 + c;
-        zh[c] = n < N ? zB[(int64_t)g * N + n] : (uint16_t)0;
-        sh16[c] = (n < N && k8 == 0) ? sB[(int64_t)g * N + n] : (uint16_t)0;
+        const int64_t gi = (int64_t)g * N + min(n0 + c, N - 1);
+        zh[c] = zB[gi];
+        sh16[c] = sB[gi];
     }
     // load: thread t takes row t / 2, dwords 8 (t % 2) .. + 7 of the tile's 64 bytes
     {
         const int r = tid >> 1, d0 = 8 * (tid & 1);
         const uint8_t* row = B + (int64_t)(k0 + r) * ldb;
+        unsigned v[8];
+        if (dw) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d)
+                v[d] = *reinterpret_cast<const unsigned*>(row + min(b0 + 4 * (d0 + d), ldb - 4));
+        } else {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                unsigned w = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w |= (unsigned)row[min(b0 + 4 * (d0 + d) + e, ldb - 1)] << (8 * e);
+                v[d] = w;
+            }
+        }
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
             const int bo = b0 + 4 * (d0 + d);
-            unsigned v = 0;
+            unsigned w = v[d];
             if (dw) {
-                if (bo < ldb) v = *reinterpret_cast<const unsigned*>(row + bo);
+                if (bo >= ldb) w = 0;
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (bo + e < ldb) v |= (unsigned)row[bo + e] << (8 * e);
+                    if (bo + e >= ldb) w &= ~(0xffu << (8 * e));
             }
-            tile[r][d0 + d] = v;
+            tile[r][d0 + d] = w;
         }
     }
     __syncthreads();
