@@ -414,23 +414,39 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
         }
         return;
     }
-    // ---- epilogue with beta: read-modify-write straight from the accumulators ----
+    // ---- epilogue with beta: read-modify-write straight from the accumulators.
+    // Half the wave tile's C at a time is loaded (clamped addresses) before
+    // any of it is stored: a load issued after a store to C waits for it, one
+    // round trip per 4 columns otherwise ----
 #pragma unroll
-    for (int j = 0; j < FM; ++j) {
-        const int gm = wrow0 + 16 * j + q;
-        if (gm >= M) continue;
+    for (int half = 0; half < 2; ++half) {
+        u32x2 old[FM / 2][FN];
 #pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            const int gn = wcol0 + 16 * i + 4 * h;
-            if (gn >= N) continue;
-            const f32x4 v = acc[8 * i + j];
-            uint16_t* dst = C + (int64_t)gm * N + gn;
-            const u32x2 c = *reinterpret_cast<const u32x2*>(dst);
-            const float r0 = fmaf(p.beta, h2f(c.x & 0xffffu), p.alpha * v[0]);
-            const float r1 = fmaf(p.beta, h2f(c.x >> 16), p.alpha * v[1]);
-            const float r2 = fmaf(p.beta, h2f(c.y & 0xffffu), p.alpha * v[2]);
-            const float r3 = fmaf(p.beta, h2f(c.y >> 16), p.alpha * v[3]);
-            *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r0, r1), pack2h(r2, r3)};
+        for (int jj = 0; jj < FM / 2; ++jj) {
+            const int gm = min(wrow0 + 16 * (half * FM / 2 + jj) + q, M - 1);
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int gn = min(wcol0 + 16 * i + 4 * h, N - 4);
+                old[jj][i] = *reinterpret_cast<const u32x2*>(C + (int64_t)gm * N + gn);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < FM / 2; ++jj) {
+            const int j = half * FM / 2 + jj;
+            const int gm = wrow0 + 16 * j + q;
+            if (gm >= M) continue;
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int gn = wcol0 + 16 * i + 4 * h;
+                if (gn >= N) continue;
+                const f32x4 v = acc[8 * i + j];
+                const u32x2 c = old[jj][i];
+                const float r0 = fmaf(p.beta, h2f(c.x & 0xffffu), p.alpha * v[0]);
+                const float r1 = fmaf(p.beta, h2f(c.x >> 16), p.alpha * v[1]);
+                const float r2 = fmaf(p.beta, h2f(c.y & 0xffffu), p.alpha * v[2]);
+                const float r3 = fmaf(p.beta, h2f(c.y >> 16), p.alpha * v[3]);
+                *reinterpret_cast<u32x2*>(C + (int64_t)gm * N + gn) = u32x2{pack2h(r0, r1), pack2h(r2, r3)};
+            }
         }
     }
 }

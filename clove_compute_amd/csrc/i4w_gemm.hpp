@@ -430,6 +430,39 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         }
         return;
     }
+    if constexpr (OUT == 1) {
+        // Y[t, o] = alpha acc + beta Y: every old value is loaded first (from a
+        // clamped address), then every result stored -- loads and stores to
+        // one array in turn would each wait for the previous round trip
+        if (p.beta != 0.0f) {
+            uint16_t old[FW][FX][16];
+#pragma unroll
+            for (int i = 0; i < FW; ++i) {
+                const int rr = min(r0 + wrow0 + 32 * i, R - 1);
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int c = c0 + wc * 32 * FX + 32 * j + 8 * (v >> 2) + 4 * h + (v & 3);
+                        old[i][j][v] = p.out[(int64_t)min(c, p.C - 1) * R + rr];
+                    }
+            }
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v)
+                        acc[i][j][v] = fmaf(p.beta, h2f(old[i][j][v]), p.alpha * acc[i][j][v]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < FW; ++i)
+#pragma unroll
+                for (int j = 0; j < FX; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = p.alpha * acc[i][j][v];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < FW; ++i) {
         const int r = r0 + wrow0 + 32 * i;
@@ -452,14 +485,8 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
                     }
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (c + e < p.C) {
-                            uint16_t* dst = p.out + (int64_t)(c + e) * R + r;
-                            float v = p.alpha * acc[i][j][4 * q + e];
-                            if (p.beta != 0.0f) v = fmaf(p.beta, h2f(*dst), v);
-                            *dst = f2h(v);
-                        }
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        if (c + e < p.C) p.out[(int64_t)(c + e) * R + r] = f2h(acc[i][j][4 * q + e]);
                 }
             }
         }

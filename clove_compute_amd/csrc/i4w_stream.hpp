@@ -299,6 +299,35 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     }
 
     // ---- epilogue: lane holds weight row r0 + 16 f + l16 and X rows 16 x + 4 h .. + 3 ----
+    if constexpr (OUT == 1) {
+        // every old value of Y first (clamped addresses), then every store: a
+        // load after a store to the same array would wait for a round trip each
+        if (p.beta != 0.0f) {
+            uint16_t old[XF][WF][4];
+#pragma unroll
+            for (int f = 0; f < WF; ++f)
+#pragma unroll
+                for (int x = 0; x < XF; ++x)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        old[x][f][e] = p.out[(int64_t)min(16 * x + 4 * h + e, p.C - 1) * R +
+                                             min(r0 + 16 * f + l16, R - 1)];
+#pragma unroll
+            for (int f = 0; f < WF; ++f)
+#pragma unroll
+                for (int x = 0; x < XF; ++x)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[x][f][e] = fmaf(p.beta, h2f(old[x][f][e]), p.alpha * acc[x][f][e]);
+        } else {
+#pragma unroll
+            for (int f = 0; f < WF; ++f)
+#pragma unroll
+                for (int x = 0; x < XF; ++x)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[x][f][e] = p.alpha * acc[x][f][e];
+        }
+    }
 #pragma unroll
     for (int f = 0; f < WF; ++f) {
         const int r = r0 + 16 * f + l16;
@@ -318,14 +347,8 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (c + e < p.C) {
-                        uint16_t* dst = p.out + (int64_t)(c + e) * R + r;
-                        float v = p.alpha * acc[x][f][e];
-                        if (p.beta != 0.0f) v = fmaf(p.beta, h2f(*dst), v);
-                        *dst = f2h(v);
-                    }
-                }
+                for (int e = 0; e < 4; ++e)
+                    if (c + e < p.C) p.out[(int64_t)(c + e) * R + r] = f2h(acc[x][f][e]);
             }
         }
     }

@@ -406,34 +406,46 @@ struct LoadI4Cols {
 // ---------------------------------------------------------------------------
 // Epilogues: called with 4 consecutive columns gn..gn+3 of row gm.
 // ---------------------------------------------------------------------------
+// Each epilogue first loads what it reads (load, for every run of the tile,
+// before any store: a load issued after a store to memory the compiler cannot
+// tell apart waits for it, one round trip per run), then stores (apply).
 template <bool ALIGNED>
 struct EpiAlphaBeta {
+    struct Pre {
+        uint16_t old[4];
+    };
+    __device__ __forceinline__ static void load(const Params& p, const uint16_t* C, int gm, int gn, Pre& pre) {
+        if (p.beta == 0.0f) return;
+        const int N = p.N;
+        const int64_t row = (int64_t)min(gm, p.M - 1) * N;
+        if constexpr (ALIGNED) {
+            const u32x2 c = *reinterpret_cast<const u32x2*>(C + row + min(gn, N - 4));
+            pre.old[0] = (uint16_t)(c.x & 0xffffu);
+            pre.old[1] = (uint16_t)(c.x >> 16);
+            pre.old[2] = (uint16_t)(c.y & 0xffffu);
+            pre.old[3] = (uint16_t)(c.y >> 16);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pre.old[e] = C[row + min(gn + e, N - 1)];
+        }
+    }
     __device__ __forceinline__ static void apply(const Params& p, uint16_t* C, int gm, int gn,
-                                                 const float acc[4]) {
+                                                 const float acc[4], const Pre& pre) {
         const int N = p.N;
         float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = p.alpha * acc[e];
+        for (int e = 0; e < 4; ++e) {
+            r[e] = p.alpha * acc[e];
+            if (p.beta != 0.0f) r[e] = fmaf(p.beta, h2f(pre.old[e]), r[e]);
+        }
         uint16_t* dst = C + (int64_t)gm * N + gn;
         if constexpr (ALIGNED) {
             if (gn >= N) return;
-            if (p.beta != 0.0f) {
-                const u32x2 c = *reinterpret_cast<const u32x2*>(dst);
-                r[0] = fmaf(p.beta, h2f(c.x & 0xffffu), r[0]);
-                r[1] = fmaf(p.beta, h2f(c.x >> 16), r[1]);
-                r[2] = fmaf(p.beta, h2f(c.y & 0xffffu), r[2]);
-                r[3] = fmaf(p.beta, h2f(c.y >> 16), r[3]);
-            }
             *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r[0], r[1]), pack2h(r[2], r[3])};
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if (gn + e < N) {
-                    float v = r[e];
-                    if (p.beta != 0.0f) v = fmaf(p.beta, h2f(dst[e]), v);
-                    dst[e] = f2h(v);
-                }
-            }
+            for (int e = 0; e < 4; ++e)
+                if (gn + e < N) dst[e] = f2h(r[e]);
         }
     }
 };
@@ -441,17 +453,21 @@ struct EpiAlphaBeta {
 // The reference kernel's epilogue (src/kernels/gemm_int4.cu:185-190): the whole
 // sum times the last group's scales, (acc * a_s) * b_s, rounded once to fp16.
 struct EpiI4Literal {
-    __device__ __forceinline__ static void apply(const Params& p, uint16_t* C, int gm, int gn,
-                                                 const float acc[4]) {
+    struct Pre {
+        float a_s, b_s[4];
+    };
+    __device__ __forceinline__ static void load(const Params& p, const uint16_t*, int gm, int gn, Pre& pre) {
         const int g = p.G - 1;
-        const float a_s = h2f(p.a_scale[(int64_t)gm * p.G + g]);
+        pre.a_s = h2f(p.a_scale[(int64_t)min(gm, p.M - 1) * p.G + g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pre.b_s[e] = h2f(p.b_scale[(int64_t)g * p.N + min(gn + e, p.N - 1)]);
+    }
+    __device__ __forceinline__ static void apply(const Params& p, uint16_t* C, int gm, int gn,
+                                                 const float acc[4], const Pre& pre) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int n = gn + e;
-            if (n < p.N) {
-                const float b_s = h2f(p.b_scale[(int64_t)g * p.N + n]);
-                C[(int64_t)gm * p.N + n] = f2h((acc[e] * a_s) * b_s);
-            }
+            if (n < p.N) C[(int64_t)gm * p.N + n] = f2h((acc[e] * pre.a_s) * pre.b_s[e]);
         }
     }
 };
@@ -639,6 +655,15 @@ __global__ void __launch_bounds__(T::NT) mfma_gemm(Params p) {
     }
 
     uint16_t* C = p.c + tc.batch * p.strideC;
+    typename EPI::Pre pre[FN][FM][4];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                EPI::load(p, C, m0 + wm * WTM + j * 32 + lrow, n0 + wn * WTN + i * 32 + q * 8 + (lane >> 5) * 4,
+                          pre[i][j][q]);
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
 #pragma unroll
@@ -650,7 +675,7 @@ __global__ void __launch_bounds__(T::NT) mfma_gemm(Params p) {
                 const int gn = n0 + wn * WTN + i * 32 + q * 8 + (lane >> 5) * 4;
                 const float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                     acc[i][j][4 * q + 3]};
-                EPI::apply(p, C, gm, gn, v);
+                EPI::apply(p, C, gm, gn, v, pre[i][j][q]);
             }
         }
     }

@@ -284,13 +284,47 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
     }
 
     // ---- epilogue: lane row m, runs of 4 columns ----
+    // Everything the epilogue reads (row / column scales, C for beta) is
+    // loaded before the first store, from clamped addresses: a load issued
+    // after a store to memory the compiler cannot tell apart waits for it, one
+    // round trip per run of 4 columns.
     unsigned char* Cb = static_cast<unsigned char*>(p.C) + batch * p.sC * (OUT == kI8Acc32 ? 4 : 2);
+    float sav[FM];
+    float sbv[FN][4][4];
+    u32x2 oldc[FM][FN][4];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int mc = min(m0 + wm * 32 * FM + 32 * j + l32, M - 1);
+        sav[j] = 1.0f;
+        if constexpr (OUT == kI8RowCol) sav[j] = h2f(p.sa[mc]);
+        if constexpr (OUT == kF16AlphaBeta) {
+            if (p.beta != 0.0f) {
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int nc = min(n0 + wn * 32 * FN + 32 * i + 8 * q + 4 * kh, N - 4);
+                        oldc[j][i][q] =
+                            *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(Cb) + (int64_t)mc * N + nc);
+                    }
+            }
+        }
+    }
+    if constexpr (OUT == kI8RowCol) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int nc = min(n0 + wn * 32 * FN + 32 * i + 8 * q + 4 * kh, N - 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sbv[i][q][e] = h2f(p.sb[nc + e]);
+            }
+    }
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
         const int m = m0 + wm * 32 * FM + 32 * j + l32;
         if (m >= M) continue;
-        float sa = 1.0f;
-        if constexpr (OUT == kI8RowCol) sa = h2f(p.sa[m]);
+        const float sa = sav[j];
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -308,7 +342,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) r[e] = p.alpha * acc[i][j][4 * q + e];
                         if (p.beta != 0.0f) {
-                            const u32x2 c = *reinterpret_cast<const u32x2*>(dst);
+                            const u32x2 c = oldc[j][i][q];
                             r[0] = fmaf(p.beta, h2f(c.x & 0xffffu), r[0]);
                             r[1] = fmaf(p.beta, h2f(c.x >> 16), r[1]);
                             r[2] = fmaf(p.beta, h2f(c.y & 0xffffu), r[2]);
@@ -319,8 +353,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
                         for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[i][j][4 * q + e]) * p.scale;
                     } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            r[e] = static_cast<float>(acc[i][j][4 * q + e]) * (sa * h2f(p.sb[n + e]));
+                        for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[i][j][4 * q + e]) * (sa * sbv[i][q][e]);
                     }
                     *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r[0], r[1]), pack2h(r[2], r[3])};
                 }
