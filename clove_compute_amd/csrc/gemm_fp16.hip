@@ -148,9 +148,13 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
             for (int s = 0; s < 16; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
-                    part[s][m] = s0 + s < p.nsplit
-                                     ? load_coherent(&ws_tile[(int64_t)(s0 + s) * MM * GV_COLS + m * GV_COLS + col])
-                                     : 0.0f;
+                    part[s][m] = load_coherent(
+                        &ws_tile[(int64_t)min(s0 + s, p.nsplit - 1) * MM * GV_COLS + m * GV_COLS + col]);
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+                    if (s0 + s >= p.nsplit) part[s][m] = 0.0f;
 #pragma unroll
             for (int s = 0; s < 16; ++s)
 #pragma unroll
@@ -159,13 +163,18 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
     }
     if (!active) return;
     if (gn < N) {
+        // beta != 0: the old outputs are loaded (clamped rows) before the first store
+        float old[MM];
+        if (p.beta != 0.0f) {
+#pragma unroll
+            for (int m = 0; m < MM; ++m) old[m] = h2f(C[(int64_t)min(m, M - 1) * N + gn]);
+        }
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
             if (m < M) {
                 float r = p.alpha * sum[m];
-                uint16_t* dst = C + (int64_t)m * N + gn;
-                if (p.beta != 0.0f) r = fmaf(p.beta, h2f(*dst), r);
-                *dst = f2h(r);
+                if (p.beta != 0.0f) r = fmaf(p.beta, old[m], r);
+                C[(int64_t)m * N + gn] = f2h(r);
             }
         }
     }

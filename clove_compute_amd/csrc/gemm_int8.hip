@@ -41,23 +41,24 @@ struct I8Params {
     unsigned* counters;
 };
 
+// one output: int32 as is, or acc * s to fp16, s = sa[m] * sb[n] (loaded by
+// the caller before its first store) for kHalfRowCol, else the tensor scale
 template <int OUT>
-__device__ __forceinline__ void int8_store(const I8Params& p, int m, int n, int acc) {
+__device__ __forceinline__ void int8_store(const I8Params& p, int m, int n, int acc, float s) {
     if constexpr (OUT == (int)Int8Out::kAcc32) {
         static_cast<int*>(p.C)[(int64_t)m * p.N + n] = acc;
     } else {
-        float s;
-        if constexpr (OUT == (int)Int8Out::kHalfRowCol) s = h2f(p.sa[m]) * h2f(p.sb[n]);
-        else s = p.scale;
+        if constexpr (OUT != (int)Int8Out::kHalfRowCol) s = p.scale;
         static_cast<uint16_t*>(p.C)[(int64_t)m * p.N + n] = f2h(static_cast<float>(acc) * s);
     }
 }
 
-// exact zero-point correction, int32 wrap-around arithmetic
-__device__ __forceinline__ int zero_correct(const I8Params& p, int acc, int m, int n) {
+// exact zero-point correction, int32 wrap-around arithmetic; rowsum = sum_k A of
+// the output's row m, colsum = sum_k B of its column n
+__device__ __forceinline__ int zero_correct(const I8Params& p, int acc, int rowsum, int colsum) {
     unsigned r = (unsigned)acc;
-    if (p.zb != 0) r -= (unsigned)p.zb * (unsigned)p.rowsum[m];
-    if (p.za != 0) r -= (unsigned)p.za * (unsigned)p.colsum[n];
+    if (p.zb != 0) r -= (unsigned)p.zb * (unsigned)rowsum;
+    if (p.za != 0) r -= (unsigned)p.za * (unsigned)colsum;
     r += (unsigned)p.K * (unsigned)p.za * (unsigned)p.zb;
     return (int)r;
 }
@@ -269,6 +270,24 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
                 }
     }
 
+    // the row / column factors of the lane's outputs first (clamped indices),
+    // then the stores: a load issued after a store waits for it
+    float rs[FM], cs[FN][16];
+    int rsum[FM], csum[FN][16];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int gm = min(m0 + wm * WTM + j * 32 + lrow, M - 1);
+        rs[j] = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sa[gm]) : 1.0f;
+        rsum[j] = p.zb != 0 ? p.rowsum[gm] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int gn = min(n0 + wn * WTN + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), N - 1);
+            cs[i][r] = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sb[gn]) : 1.0f;
+            csum[i][r] = p.za != 0 ? p.colsum[gn] : 0;
+        }
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -278,7 +297,8 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int gn = n0 + wn * WTN + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (gn < N) int8_store<OUT>(p, gm, gn, zero_correct(p, acc[i][j][r], gm, gn));
+                if (gn >= N) continue;
+                int8_store<OUT>(p, gm, gn, zero_correct(p, acc[i][j][r], rsum[j], csum[i][r]), rs[j] * cs[i][r]);
             }
         }
 }
@@ -389,9 +409,13 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
             for (int s = 0; s < 16; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
-                    part[s][m] = s0 + s < p.nsplit ? __float_as_int(load_coherent(
-                                                         &ws_tile[(int64_t)(s0 + s) * MM * IV_COLS + m * IV_COLS + col]))
-                                                   : 0;
+                    part[s][m] = __float_as_int(load_coherent(
+                        &ws_tile[(int64_t)min(s0 + s, p.nsplit - 1) * MM * IV_COLS + m * IV_COLS + col]));
+#pragma unroll
+            for (int s = 0; s < 16; ++s)
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+                    if (s0 + s >= p.nsplit) part[s][m] = 0;
 #pragma unroll
             for (int s = 0; s < 16; ++s)
 #pragma unroll
@@ -399,9 +423,15 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
         }
     }
     if (active && gn < N) {
+        // every scale the stores use is loaded before the first store
+        float rs[MM];
+        const float cs = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sb[gn]) : 1.0f;
 #pragma unroll
         for (int m = 0; m < MM; ++m)
-            if (m < M) int8_store<OUT>(p, m, gn, sum[m]);
+            rs[m] = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sa[min(m, M - 1)]) : 1.0f;
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+            if (m < M) int8_store<OUT>(p, m, gn, sum[m], rs[m] * cs);
     }
 }
 

@@ -217,6 +217,14 @@ __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_ge
         }
         return;
     }
+    // beta != 0: every old output of the lane is loaded (clamped indices)
+    // before the first store, since a load issued after a store waits for it
+    float old[RPW];
+    if (p.beta != 0.0f) {
+        const uint16_t* src = p.Y + (int64_t)min(lane, p.T - 1) * p.O;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) old[r] = h2f(src[min(row0 + r, p.O - 1)]);
+    }
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
@@ -225,10 +233,9 @@ __global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_ge
 #pragma unroll
         for (int t = 0; t < TV; ++t)
             if (t == lane) v = acc[r][t];
-        uint16_t* dst = p.Y + (int64_t)lane * p.O + row;
         float y = p.alpha * v;
-        if (p.beta != 0.0f) y = fmaf(p.beta, h2f(*dst), y);
-        *dst = f2h(y);
+        if (p.beta != 0.0f) y = fmaf(p.beta, old[r], y);
+        p.Y[(int64_t)lane * p.O + row] = f2h(y);
     }
 }
 
