@@ -299,7 +299,7 @@ int main() {
     fp16_case("test_gemm_large 1024^3", 1024, 1024, 1024, 1.0f, 0.0f, 3);
     fp16_case("test_gemm_nonsquare 128x4096x4096", 128, 4096, 4096, 1.0f, 0.0f, 4);
     fp16_case("test_gemm_decode 1x4096x4096", 1, 4096, 4096, 1.0f, 0.0f, 5);
-    fp16_case("test_gemm_alpha_beta 256^3 (0.5, 0.5)", 256, 256, 256, 0.5f, 0.5f, 6);
+    fp16_case("test_gemm_alpha_beta 128^3 (0.5, 0.25)", 128, 128, 128, 0.5f, 0.25f, 6);
     fp16_default_args_case();
     batched_case();
     int8_case(64, 64, 64);
