@@ -42,6 +42,13 @@ struct BufferEntry {
 };
 std::map<std::tuple<int, void*, int>, BufferEntry> g_buffers;  // guarded by g_scratch_mu
 
+// Buffers replaced by larger ones, per device, freed by clove_release_scratch
+// (after a device synchronize).  A replaced buffer is not freed on the spot: a
+// call on another host thread may have taken it and not yet launched the
+// kernel that uses it.  Sizes grow by powers of two, so the retired buffers
+// of a stream add up to less than its current one.
+std::map<int, std::vector<void*>> g_retired;  // guarded by g_scratch_mu
+
 __global__ void zero_u16(uint16_t* p, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
@@ -97,14 +104,13 @@ clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t 
     }
     const size_t pb = round_up_pow2(partial_bytes, (size_t)4 << 20);
     const size_t nc = round_up_pow2(num_counters, 4096);
-    if (e.base) {
-        // in-flight work on this stream may still use the old buffer
-        if (hipStreamSynchronize(stream) != hipSuccess) return CLOVE_ERR_LAUNCH;
-        (void)hipFree(e.base);
-        e = ScratchEntry{};
-    }
     void* base = nullptr;
     if (hipMalloc(&base, pb + nc * sizeof(unsigned)) != hipSuccess) return CLOVE_ERR_OUT_OF_MEMORY;
+    if (e.base) {
+        // queued work (and calls of other host threads) may still use the old buffer
+        g_retired[dev].push_back(e.base);
+        e = ScratchEntry{};
+    }
     unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(base) + pb);
     hipLaunchKernelGGL(zero_u32, dim3(64), dim3(256), 0, stream, counters, nc);
     if (hipGetLastError() != hipSuccess) {
@@ -130,15 +136,10 @@ clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void**
         return CLOVE_OK;
     }
     const size_t nb = round_up_pow2(bytes, (size_t)1 << 20);
-    if (e.base) {
-        if (hipStreamSynchronize(stream) != hipSuccess) return CLOVE_ERR_LAUNCH;
-        (void)hipFree(e.base);
-        e = BufferEntry{};
-    }
-    if (hipMalloc(&e.base, nb) != hipSuccess) {
-        e = BufferEntry{};
-        return CLOVE_ERR_OUT_OF_MEMORY;
-    }
+    void* base = nullptr;
+    if (hipMalloc(&base, nb) != hipSuccess) return CLOVE_ERR_OUT_OF_MEMORY;
+    if (e.base) g_retired[dev].push_back(e.base);  // as in acquire_scratch
+    e.base = base;
     e.bytes = nb;
     *out = e.base;
     return CLOVE_OK;
@@ -393,6 +394,8 @@ clove_status_t clove_release_scratch(void) {
             ++it;
         }
     }
+    for (void* p : g_retired[dev]) (void)hipFree(p);
+    g_retired.erase(dev);
     return CLOVE_OK;
 }
 

@@ -14,7 +14,11 @@
  * Scratch: split-K launches keep a per-(device, stream) scratch buffer that
  * the library allocates on first use (hipMalloc) and keeps until
  * clove_release_scratch() or process exit.  Calls on different streams never
- * share scratch; calls on one stream are ordered by the stream.
+ * share scratch; calls on one stream are ordered by the stream.  A call that
+ * needs more scratch than the stream holds allocates a larger buffer (twice
+ * the size or more) and keeps the old one until clove_release_scratch(), so
+ * that calls of other host threads on the same stream that already took it
+ * stay valid; no call synchronises a stream.
  */
 #ifndef CLOVE_GEMM_C_H
 #define CLOVE_GEMM_C_H
@@ -191,8 +195,9 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
                                   void* stream);
 
 /* Frees the scratch buffers held for the current device (all streams),
- * including the SwiGLU intermediates.  Synchronises the device first.  No
- * reference counterpart. */
+ * including the SwiGLU intermediates and buffers replaced by larger ones.
+ * Synchronises the device first; no other call may be using the library on
+ * this device meanwhile.  No reference counterpart. */
 clove_status_t clove_release_scratch(void);
 
 #ifdef __cplusplus
