@@ -111,13 +111,24 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
     constexpr int BCH = 2;  // B chunks per thread in the fast path
     const bool bfast = p.ldb == 1 && NV <= 2 && nch <= BCH * NT &&
                        (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 && (K & 31) == 0;
+    // (with their groups' B scales and zero points: loaded here, not where the
+    // chunk constants are formed, where they would be a second round trip)
     u32x4 braw[BCH][2];
+    uint16_t bzr[BCH][NV], bsr[BCH][NV];
     if (bfast) {
 #pragma unroll
         for (int i = 0; i < BCH; ++i) {
             const int c = min(tid + i * NT, nch - 1);  // unconditional, see below
             braw[i][0] = *reinterpret_cast<const u32x4*>(p.B + 32 * c);
             braw[i][1] = *reinterpret_cast<const u32x4*>(p.B + 32 * c + 16);
+            if constexpr (MODE == mg::kI4Groupwise) {
+#pragma unroll
+                for (int n = 0; n < NV; ++n) {
+                    const int64_t gi = (int64_t)(c >> 2) * p.N + min(n, p.N - 1);
+                    bzr[i][n] = p.B_zero[gi];
+                    bsr[i][n] = p.B_scale[gi];
+                }
+            }
         }
     }
 
@@ -161,16 +172,24 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
 
     // ---- stage B once per workgroup ----
     // per-chunk constants of column n (see the LDS layout)
-    auto chunk_consts = [&](int n, int c, unsigned sb) -> i32x4 {
+    // (zraw, sraw: column n's B zero point and scale for chunk c's group)
+    auto chunk_consts_v = [&](int n, int c, unsigned sb, uint16_t zraw, uint16_t sraw) -> i32x4 {
         const int cnt = min(32, K - 32 * c);
         if constexpr (MODE == mg::kI4Groupwise) {
-            const int g = c >> 2;
             const bool in = n < p.N;
-            const int zb = in ? (int)rintf(h2f(p.B_zero[(int64_t)g * p.N + n])) : 0;
-            const float sbf = in ? h2f(p.B_scale[(int64_t)g * p.N + n]) : 0.0f;
+            const int zb = in ? (int)rintf(h2f(zraw)) : 0;
+            const float sbf = in ? h2f(sraw) : 0.0f;
             return i32x4{zb, (int)sb - cnt * zb, bitcast<int>(sbf), 0};
         } else {
             return i32x4{64 * cnt - 8 * (int)sb, 0, 0, 0};
+        }
+    };
+    auto chunk_consts = [&](int n, int c, unsigned sb) -> i32x4 {
+        if constexpr (MODE == mg::kI4Groupwise) {
+            const int64_t gi = (int64_t)(c >> 2) * p.N + min(n, p.N - 1);
+            return chunk_consts_v(n, c, sb, p.B_zero[gi], p.B_scale[gi]);
+        } else {
+            return chunk_consts_v(n, c, sb, 0, 0);
         }
     };
     if (bfast) {
@@ -197,7 +216,8 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
                 sb = __builtin_amdgcn_udot8(w[1], kOnes, sb, false);
                 sb = __builtin_amdgcn_udot8(w[2], kOnes, sb, false);
                 sb = __builtin_amdgcn_udot8(w[3], kOnes, sb, false);
-                Bc[n * nch + c] = chunk_consts(n, c, sb);
+                if constexpr (MODE == mg::kI4Groupwise) Bc[n * nch + c] = chunk_consts_v(n, c, sb, bzr[i][n], bsr[i][n]);
+                else Bc[n * nch + c] = chunk_consts_v(n, c, sb, 0, 0);
             }
         }
         lds_barrier();
