@@ -34,3 +34,29 @@ def test_scratch_growth_and_release():
     print("scratch: after release", flush=True)
     _check(cg, 128, 4096, 4096, 3)
     _check(cg, 32, 4096, 4096, 4)
+
+
+def test_two_streams_keep_separate_scratch():
+    # split-K launches on two streams at once: each stream has its own partials
+    # and counters, so neither result is disturbed by the other
+    import torch
+    import clove_compute_amd as cg
+    M, N, K = 32, 4096, 4096
+    ins, outs, streams = [], [], [torch.cuda.Stream(), torch.cuda.Stream()]
+    for key in range(2):
+        g = rng("scratch2", key)
+        A = g.standard_normal((M, K)).astype(np.float16)
+        B = (g.standard_normal((K, N)) * 0.02).astype(np.float16)
+        ins.append((A, B, to_dev(A), to_dev(B)))
+        outs.append(empty_f16(M, N))
+    torch.cuda.synchronize()
+    print("scratch: 2 streams x 4 calls", flush=True)
+    for _ in range(4):
+        for s, (_, _, dA, dB), C in zip(streams, ins, outs):
+            with torch.cuda.stream(s):
+                cg.gemm_fp16(dA, dB, C, M, N, K, stream=s)
+    torch.cuda.synchronize()
+    for (A, B, _, _), C in zip(ins, outs):
+        rows = np.array([0, 7, 19, M - 1])
+        ok, rep = within_tol(to_host(C)[rows], oracle.gemm_fp16_f64(A[rows], B))
+        assert ok, rep
