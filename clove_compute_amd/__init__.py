@@ -5,7 +5,10 @@ include/clove/gemm_c.h, C++ spelling in include/clove/gemm.h).  This package
 is its Python host side: the ctypes binding, a mirror of the reference's
 GEMM API over torch device tensors, and the INT4 packing/quantisation helpers.
 """
-from ._lib import CloveError, CLOVE_INT4_GROUPWISE, CLOVE_INT4_REFERENCE_LITERAL  # noqa: F401
+from ._lib import (  # noqa: F401
+    CloveError, CLOVE_ERR_WORKSPACE, CLOVE_INT4_GROUPWISE, CLOVE_INT4_REFERENCE_LITERAL,
+    CLOVE_WORKSPACE_MIN_BYTES,
+)
 from .gemm import (  # noqa: F401
     INT4_GROUP_SIZE,
     gemm_fp16,
@@ -20,5 +23,7 @@ from .gemm import (  # noqa: F401
     swiglu,
     swiglu_fused,
     w4a16_swiglu,
+    workspace_bind,
+    workspace_query,
 )
 from . import quant  # noqa: F401

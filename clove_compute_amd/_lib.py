@@ -19,6 +19,9 @@ CLOVE_ERR_ALIASING = 4
 CLOVE_ERR_OUT_OF_MEMORY = 5
 CLOVE_ERR_LAUNCH = 6
 CLOVE_ERR_NO_DEVICE = 7
+CLOVE_ERR_WORKSPACE = 8
+
+CLOVE_WORKSPACE_MIN_BYTES = 65536
 
 CLOVE_INT4_GROUPWISE = 0
 CLOVE_INT4_REFERENCE_LITERAL = 1
@@ -43,6 +46,9 @@ SIGNATURES = {
     "clove_swiglu": ([P, P, P, I, P], I),
     "clove_swiglu_fused": ([P, P, P, P, I, I, I, P], I),
     "clove_w4a16_swiglu": ([P, P, P, P, P, I, I, I, P], I),
+    "clove_workspace_bind": ([P, ctypes.c_size_t], I),
+    "clove_workspace_query_begin": ([], I),
+    "clove_workspace_query_end": ([], ctypes.c_size_t),
     "clove_release_scratch": ([], I),
 }
 

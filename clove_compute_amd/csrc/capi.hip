@@ -73,7 +73,50 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
 
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 
+// ---------------------------------------------------------------------------
+// caller-owned workspace (clove_workspace_bind / clove_workspace_query_*), per
+// host thread.  Layout of a bound workspace: the completion counters at its
+// start (a fixed region, so a counter never lands where an earlier call left
+// partial sums), then each acquisition of the call at 256-byte offsets.
+// ---------------------------------------------------------------------------
+enum class WsMode { kLibrary, kBound, kQuery };
+struct ThreadWs {
+    WsMode mode = WsMode::kLibrary;
+    char* ptr = nullptr;
+    size_t bytes = 0;
+    size_t used = 0;  // carve offset of the current call
+    size_t need = 0;  // query: the largest call so far
+};
+thread_local ThreadWs t_ws;
+thread_local ThreadWs t_ws_saved;  // the mode a query interrupted
+constexpr size_t kWsCounterBytes = CLOVE_WORKSPACE_MIN_BYTES;
+constexpr size_t kWsCounters = kWsCounterBytes / sizeof(unsigned);
+
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Carves `bytes` for the current call; nullptr-based in a query (nothing is
+// launched, so nothing reads it).
+clove_status_t ws_carve(size_t bytes, char** out) {
+    const size_t off = t_ws.used;
+    t_ws.used += round256(bytes);
+    if (t_ws.mode == WsMode::kBound && t_ws.used > t_ws.bytes) return CLOVE_ERR_WORKSPACE;
+    *out = reinterpret_cast<char*>(reinterpret_cast<uintptr_t>(t_ws.ptr) + off);
+    return CLOVE_OK;
+}
+
+// One per C entry point that dispatches: starts the call's carving after the
+// counters and, in a query, records what the call took.
+struct CallScope {
+    CallScope() { t_ws.used = kWsCounterBytes; }
+    ~CallScope() {
+        if (t_ws.mode == WsMode::kQuery && t_ws.used > kWsCounterBytes && t_ws.used > t_ws.need)
+            t_ws.need = t_ws.used;
+    }
+};
+
 }  // namespace
+
+bool dry_run() { return t_ws.mode == WsMode::kQuery; }
 
 clove_status_t current_device_info(DeviceInfo* out) {
     int dev = 0;
@@ -94,6 +137,17 @@ clove_status_t current_device_info(DeviceInfo* out) {
 
 clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t num_counters,
                                Scratch* out) {
+    if (t_ws.mode != WsMode::kLibrary) {
+        if (num_counters > kWsCounters) return CLOVE_ERR_WORKSPACE;
+        char* part = nullptr;
+        const clove_status_t st = ws_carve(partial_bytes, &part);
+        if (st != CLOVE_OK) return st;
+        out->partials = reinterpret_cast<float*>(part);
+        out->partial_bytes = round256(partial_bytes);
+        out->counters = reinterpret_cast<unsigned*>(t_ws.ptr);
+        out->num_counters = kWsCounters;
+        return CLOVE_OK;
+    }
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -127,6 +181,12 @@ clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t 
 }
 
 clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void** out) {
+    if (t_ws.mode != WsMode::kLibrary) {
+        char* p = nullptr;
+        const clove_status_t st = ws_carve(bytes, &p);
+        *out = p;
+        return st;
+    }
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -161,6 +221,7 @@ const char* clove_status_string(clove_status_t status) {
         case CLOVE_ERR_OUT_OF_MEMORY: return "CLOVE_ERR_OUT_OF_MEMORY: scratch allocation failed";
         case CLOVE_ERR_LAUNCH: return "CLOVE_ERR_LAUNCH: kernel launch failed";
         case CLOVE_ERR_NO_DEVICE: return "CLOVE_ERR_NO_DEVICE: no usable HIP device";
+        case CLOVE_ERR_WORKSPACE: return "CLOVE_ERR_WORKSPACE: the bound workspace is too small for the call";
     }
     return "CLOVE_ERR_UNKNOWN";
 }
@@ -169,6 +230,7 @@ int clove_abi_version(void) { return kAbiVersion; }
 
 clove_status_t clove_gemm_fp16_batched(const void* A, const void* B, void* C, int batch, int M,
                                        int N, int K, float alpha, float beta, void* stream) {
+    CallScope scope;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
     if (batch == 0 || M == 0 || N == 0) return CLOVE_OK;
     if (!C || (K > 0 && (!A || !B))) return CLOVE_ERR_NULL_POINTER;
@@ -189,6 +251,7 @@ clove_status_t clove_gemm_fp16(const void* A, const void* B, void* C, int M, int
 }
 
 static clove_status_t int8_common(Int8Args& a, void* stream) {
+    CallScope scope;
     if (a.M < 0 || a.N < 0 || a.K < 0) return CLOVE_ERR_INVALID_DIM;
     if (a.M == 0 || a.N == 0) return CLOVE_OK;
     if (!a.C || (a.K > 0 && (!a.A || !a.B))) return CLOVE_ERR_NULL_POINTER;
@@ -243,6 +306,7 @@ clove_status_t clove_gemm_int4_ex(const uint8_t* A_q, const void* A_scale, const
                                   const uint8_t* B_q, const void* B_scale, const void* B_zero,
                                   void* C, int M, int N, int K, clove_int4_mode_t mode,
                                   void* stream) {
+    CallScope scope;
     if (mode != CLOVE_INT4_GROUPWISE && mode != CLOVE_INT4_REFERENCE_LITERAL)
         return CLOVE_ERR_INVALID_ARG;
     if (M < 0 || N < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
@@ -289,6 +353,7 @@ clove_status_t clove_gemm_int4(const uint8_t* A_q, const void* A_scale, const vo
 clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q, const void* W_scale,
                                 const void* W_zero, void* Y, int T, int O, int K, float alpha,
                                 float beta, void* stream) {
+    CallScope scope;
     if (T < 0 || O < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
     if (K % 2 != 0) return CLOVE_ERR_INVALID_ARG;
     if (T == 0 || O == 0) return CLOVE_OK;
@@ -316,6 +381,7 @@ static bool same_or_disjoint(const void* a, const void* b, size_t bytes) {
 }
 
 clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int size, void* stream) {
+    CallScope scope;
     if (size < 0) return CLOVE_ERR_INVALID_DIM;
     if (size == 0) return CLOVE_OK;
     if (!gate || !up || !output) return CLOVE_ERR_NULL_POINTER;
@@ -329,6 +395,7 @@ clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int 
 
 clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const void* W_up, void* output,
                                   int batch_seq, int hidden_dim, int intermediate_dim, void* stream) {
+    CallScope scope;
     const int T = batch_seq, H = hidden_dim, I = intermediate_dim;
     if (T < 0 || H < 0 || I < 0) return CLOVE_ERR_INVALID_DIM;
     if (T == 0 || I == 0) return CLOVE_OK;
@@ -347,6 +414,7 @@ clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const v
 
 clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void* W_scale,
                                   const void* W_zero, void* H, int T, int I, int K, void* stream) {
+    CallScope scope;
     if (T < 0 || I < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
     if (K % 2 != 0) return CLOVE_ERR_INVALID_ARG;
     if (T == 0 || I == 0) return CLOVE_OK;
@@ -360,7 +428,7 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
         return CLOVE_ERR_ALIASING;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (K == 0) {  // gate = up = 0: swiglu(0, 0) = +0
-        hipLaunchKernelGGL(zero_u16, dim3(256), dim3(256), 0, s, static_cast<uint16_t*>(H), (size_t)T * I);
+        CLOVE_LAUNCH(zero_u16, dim3(256), dim3(256), 0, s, static_cast<uint16_t*>(H), (size_t)T * I);
         return check_launch();
     }
     W4A16Args a;
@@ -371,6 +439,38 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
     a.Y = static_cast<uint16_t*>(H);
     a.T = T; a.O = I; a.K = K;
     return launch_w4a16_swiglu(a, s);
+}
+
+clove_status_t clove_workspace_bind(void* ptr, size_t bytes) {
+    if (t_ws.mode == WsMode::kQuery) return CLOVE_ERR_INVALID_ARG;
+    if (!ptr) {
+        if (bytes != 0) return CLOVE_ERR_NULL_POINTER;
+        t_ws = ThreadWs{};
+        return CLOVE_OK;
+    }
+    if ((reinterpret_cast<uintptr_t>(ptr) & 255u) != 0) return CLOVE_ERR_INVALID_ARG;
+    if (bytes < kWsCounterBytes) return CLOVE_ERR_WORKSPACE;
+    t_ws = ThreadWs{};
+    t_ws.mode = WsMode::kBound;
+    t_ws.ptr = static_cast<char*>(ptr);
+    t_ws.bytes = bytes;
+    return CLOVE_OK;
+}
+
+clove_status_t clove_workspace_query_begin(void) {
+    if (t_ws.mode == WsMode::kQuery) return CLOVE_ERR_INVALID_ARG;
+    t_ws_saved = t_ws;
+    t_ws = ThreadWs{};
+    t_ws.mode = WsMode::kQuery;
+    return CLOVE_OK;
+}
+
+size_t clove_workspace_query_end(void) {
+    if (t_ws.mode != WsMode::kQuery) return 0;
+    const size_t need = t_ws.need;
+    t_ws = t_ws_saved;
+    t_ws_saved = ThreadWs{};
+    return need;
 }
 
 clove_status_t clove_release_scratch(void) {

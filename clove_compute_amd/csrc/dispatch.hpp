@@ -22,9 +22,21 @@ struct Scratch {
 };
 
 // Returns scratch with at least the requested capacity for `stream` on the
-// current device (implemented in capi.hip).
+// current device (implemented in capi.hip): library-owned, or carved from the
+// workspace the calling thread has bound (clove_workspace_bind), or, in a
+// workspace size query, a placeholder that only records the size.
 clove_status_t acquire_scratch(hipStream_t stream, size_t partial_bytes, size_t num_counters,
                                Scratch* out);
+
+// True while the calling thread runs a workspace size query: calls plan and
+// size their scratch but launch nothing.
+bool dry_run();
+
+// Every kernel launch of the library goes through this.
+#define CLOVE_LAUNCH(...)                                   \
+    do {                                                    \
+        if (!::clove::dry_run()) hipLaunchKernelGGL(__VA_ARGS__); \
+    } while (0)
 
 struct DeviceInfo {
     int device = 0;
@@ -99,8 +111,8 @@ clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gat
                                         uint16_t* out, int T, int hidden, int inter, hipStream_t stream);
 
 // A device buffer of at least `bytes` owned by the library per (device,
-// stream, slot), kept across calls (capi.hip); slot 0 is reserved for the
-// split-K scratch.  Synchronises the stream when it has to grow.
+// stream, slot), kept across calls (capi.hip), or carved from the bound
+// workspace as acquire_scratch; slot 0 is reserved for the split-K scratch.
 clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void** out);
 constexpr int kBufSwiglu = 1;  // gate / up intermediates of the unfused SwiGLU paths
 

@@ -211,10 +211,10 @@ clove_status_t run_mfma(Params p, int batch, int num_cus, hipStream_t stream) {
     const int64_t grid = (int64_t)tiles * p.nsplit;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
     if (p.nsplit > 1)
-        hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, true>),
+        CLOVE_LAUNCH((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, true>),
                            dim3((unsigned)grid), dim3(T::NT), 0, stream, p);
     else
-        hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, false>),
+        CLOVE_LAUNCH((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldNone, false>),
                            dim3((unsigned)grid), dim3(T::NT), 0, stream, p);
     return check_launch();
 }
@@ -236,7 +236,7 @@ clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int ba
                 cdiv(M, BigTile::BM), cdiv(N, BigTile::BN)};
     const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * batch;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
-    hipLaunchKernelGGL(dma::gemm_f16_big<dma::Big>, dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
+    CLOVE_LAUNCH(dma::gemm_f16_big<dma::Big>, dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
     return check_launch();
 }
 
@@ -257,7 +257,7 @@ clove_status_t run_gemv(GemvParams p, int batch, hipStream_t stream) {
     }
     const int64_t grid = (int64_t)tiles * p.nsplit;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
-    hipLaunchKernelGGL((gemv_f16<MM>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
+    CLOVE_LAUNCH((gemv_f16<MM>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
     return check_launch();
 }
 

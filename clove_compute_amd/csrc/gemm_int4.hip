@@ -354,7 +354,7 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, grid, dim3(wpb * 64), lds, stream, p);
+    CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
 }
 
@@ -405,7 +405,7 @@ clove_status_t run_mfma(mg::Params p, int cus, hipStream_t stream) {
         p.counters = s.counters;
     }
     constexpr int FOLD = MODE == mg::kI4Literal ? mg::kFoldNone : mg::kFoldAB;
-    hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, EPI, FOLD>), dim3(tiles * p.nsplit), dim3(T::NT), 0,
+    CLOVE_LAUNCH((mg::mfma_gemm<T, LA, LB, EPI, FOLD>), dim3(tiles * p.nsplit), dim3(T::NT), 0,
                        stream, p);
     return check_launch();
 }
@@ -434,7 +434,7 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
     if (a.K == 0) {
         // empty sum: +0 in both modes (the reference reads no scale group then)
         const size_t n = (size_t)a.M * a.N;
-        hipLaunchKernelGGL(fill_u16, dim3((unsigned)(n < 1048576 ? cdiv64(n, 256) : 4096)), dim3(256), 0,
+        CLOVE_LAUNCH(fill_u16, dim3((unsigned)(n < 1048576 ? cdiv64(n, 256) : 4096)), dim3(256), 0,
                            stream, a.C, n, (uint16_t)0);
         return check_launch();
     }

@@ -457,9 +457,9 @@ clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     const int64_t g = (int64_t)col_blocks * p.nsplit;
     if (g > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
     const dim3 grid((unsigned)g);
-    if (p.M == 1) hipLaunchKernelGGL((int8_gemv<1, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
-    else if (p.M == 2) hipLaunchKernelGGL((int8_gemv<2, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
-    else hipLaunchKernelGGL((int8_gemv<4, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
+    if (p.M == 1) CLOVE_LAUNCH((int8_gemv<1, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
+    else if (p.M == 2) CLOVE_LAUNCH((int8_gemv<2, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
+    else CLOVE_LAUNCH((int8_gemv<4, OUT>), grid, dim3(1024), 0, stream, p, col_blocks);
     return check_launch();
 }
 
@@ -484,13 +484,13 @@ clove_status_t run_mfma(I8Params p, int cus, hipStream_t stream) {
         if (sums) {
             int* rs = reinterpret_cast<int*>(reinterpret_cast<char*>(s.partials) + part);
             int* cs = rs + p.M;
-            hipLaunchKernelGGL(int8_rowsum, dim3(cdiv(p.M, 4)), dim3(256), 0, stream, p.A, p.M, p.K, rs);
-            hipLaunchKernelGGL(int8_colsum, dim3(cdiv(p.N, 256)), dim3(256), 0, stream, p.B, p.N, p.K, cs);
+            CLOVE_LAUNCH(int8_rowsum, dim3(cdiv(p.M, 4)), dim3(256), 0, stream, p.A, p.M, p.K, rs);
+            CLOVE_LAUNCH(int8_colsum, dim3(cdiv(p.N, 256)), dim3(256), 0, stream, p.B, p.N, p.K, cs);
             p.rowsum = rs;
             p.colsum = cs;
         }
     }
-    hipLaunchKernelGGL((int8_mfma<BM, BN, BK, WGM, WGN, OUT, ALIGNED>), dim3(tiles * p.nsplit),
+    CLOVE_LAUNCH((int8_mfma<BM, BN, BK, WGM, WGN, OUT, ALIGNED>), dim3(tiles * p.nsplit),
                        dim3(WGM * WGN * 64), 0, stream, p);
     return check_launch();
 }

@@ -69,7 +69,7 @@ clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_byt
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, dim3((unsigned)(tiles * pl.nsplit)), dim3(CF::NT), lds, stream, a);
+    CLOVE_LAUNCH(k, dim3((unsigned)(tiles * pl.nsplit)), dim3(CF::NT), lds, stream, a);
     return check_launch();
 }
 
@@ -103,7 +103,7 @@ clove_status_t launch_stream(const Args& a, hipStream_t stream) {
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
             hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream, a);
+    CLOVE_LAUNCH(k, dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream, a);
     return check_launch();
 }
 
@@ -203,7 +203,7 @@ bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t
     auto prep = [&](Args& args, char* extra) -> clove_status_t {
         uint16_t* xt = reinterpret_cast<uint16_t*>(extra);
         float* xs = reinterpret_cast<float*>(extra + xt_bytes);
-        hipLaunchKernelGGL(i4w_prep_b, dim3((unsigned)G, (unsigned)cdiv(Npad, 128)), dim3(256), 0, stream, q.B,
+        CLOVE_LAUNCH(i4w_prep_b, dim3((unsigned)G, (unsigned)cdiv(Npad, 128)), dim3(256), 0, stream, q.B,
                            ldb, q.B_scale, q.B_zero, q.N, q.K, G, Npad, xt, xs);
         args.X = xt;
         args.xs = xs;

@@ -43,7 +43,7 @@ clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             CF::LDS) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, dim3((unsigned)(tiles * a.nsplit)), dim3(CF::NT), CF::LDS, stream, a);
+    CLOVE_LAUNCH(k, dim3((unsigned)(tiles * a.nsplit)), dim3(CF::NT), CF::LDS, stream, a);
     return check_launch();
 }
 

@@ -57,7 +57,7 @@ clove_status_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t*
     const int64_t work = vec ? hw::cdiv64(n, 8) : n;
     // enough workgroups to keep every CU streaming, capped at 16 per CU
     const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(hw::cdiv64(work, 256), 16 * dev.num_cus));
-    hipLaunchKernelGGL(act::swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, gate, up, out, n,
+    CLOVE_LAUNCH(act::swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, gate, up, out, n,
                        vec ? 1 : 0);
     return check_launch();
 }

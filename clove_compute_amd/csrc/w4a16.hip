@@ -272,7 +272,7 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
         hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
         return CLOVE_ERR_LAUNCH;
-    hipLaunchKernelGGL(k, grid, dim3(wpb * 64), lds, stream, p);
+    CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
 }
 
@@ -322,7 +322,7 @@ clove_status_t run_mfma(mg::Params p, int cus, hipStream_t stream) {
         p.ws = s.partials;
         p.counters = s.counters;
     }
-    hipLaunchKernelGGL((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldB>), dim3(tiles * p.nsplit),
+    CLOVE_LAUNCH((mg::mfma_gemm<T, LA, LB, mg::EpiAlphaBeta<ALIGNED>, mg::kFoldB>), dim3(tiles * p.nsplit),
                        dim3(T::NT), 0, stream, p);
     return check_launch();
 }

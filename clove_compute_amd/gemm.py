@@ -120,5 +120,27 @@ def w4a16_swiglu(X, W_q, W_scale, W_zero, H, T: int, I: int, K: int, stream=None
                                              _ptr(H), T, I, K, _stream(stream)), "w4a16_swiglu")
 
 
+def workspace_bind(workspace=None, nbytes: int = 0) -> None:
+    """Bind a caller-owned workspace (a device tensor or pointer; 256-byte aligned, its first
+    CLOVE_WORKSPACE_MIN_BYTES zero) to the calling thread; ``workspace_bind()`` unbinds."""
+    if workspace is not None and not isinstance(workspace, int) and nbytes == 0:
+        nbytes = workspace.numel() * workspace.element_size()
+    _lib.check(_lib.lib().clove_workspace_bind(_ptr(workspace), nbytes), "workspace_bind")
+
+
+class workspace_query:
+    """``with workspace_query() as q: <calls>`` plans the calls without launching them;
+    ``q.bytes`` is then the largest workspace any of them needs (0: none)."""
+
+    def __enter__(self):
+        _lib.check(_lib.lib().clove_workspace_query_begin(), "workspace_query_begin")
+        self.bytes = 0
+        return self
+
+    def __exit__(self, *exc):
+        self.bytes = int(_lib.lib().clove_workspace_query_end())
+        return False
+
+
 def release_scratch() -> None:
     _lib.check(_lib.lib().clove_release_scratch(), "release_scratch")

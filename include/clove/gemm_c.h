@@ -23,6 +23,7 @@
 #ifndef CLOVE_GEMM_C_H
 #define CLOVE_GEMM_C_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -37,7 +38,8 @@ typedef enum clove_status {
     CLOVE_ERR_ALIASING = 4,       /* the output overlaps an input */
     CLOVE_ERR_OUT_OF_MEMORY = 5,  /* scratch allocation failed */
     CLOVE_ERR_LAUNCH = 6,         /* the HIP runtime rejected a launch */
-    CLOVE_ERR_NO_DEVICE = 7       /* no usable HIP device */
+    CLOVE_ERR_NO_DEVICE = 7,      /* no usable HIP device */
+    CLOVE_ERR_WORKSPACE = 8       /* the bound workspace is too small for the call */
 } clove_status_t;
 
 /* INT4 arithmetic selected by clove_gemm_int4_ex. */
@@ -193,6 +195,31 @@ clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const v
 clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void* W_scale,
                                   const void* W_zero, void* H, int T, int I, int K,
                                   void* stream);
+
+/* Caller-owned workspace (no reference counterpart: the reference allocates no
+ * scratch).  Per host thread, three modes:
+ *
+ *  - library scratch (the default): the per-(device, stream) buffers above;
+ *  - a bound workspace, clove_workspace_bind(ptr, bytes): calls on this thread
+ *    take their split-K partials, completion counters and intermediates from
+ *    [ptr, ptr + bytes) and allocate nothing; a call that needs more returns
+ *    CLOVE_ERR_WORKSPACE and launches nothing.  ptr must be 256-byte aligned
+ *    and bytes >= CLOVE_WORKSPACE_MIN_BYTES; the first CLOVE_WORKSPACE_MIN_BYTES
+ *    (the counters) must be zero before the first call, and every call leaves
+ *    them zero.  Calls that may run at the same time on the device (other
+ *    streams, other threads) must not share a workspace.
+ *    clove_workspace_bind(NULL, 0) returns to library scratch;
+ *  - a size query: between clove_workspace_query_begin() and
+ *    clove_workspace_query_end(), calls on this thread validate their
+ *    arguments and plan their launches but launch nothing and allocate
+ *    nothing; query_end returns the largest workspace any of them needs
+ *    (0 if none needs one) and restores the previous mode.  A query plans
+ *    with the pointers it is given (alignment selects kernels), so pass the
+ *    ones the real call will use. */
+#define CLOVE_WORKSPACE_MIN_BYTES ((size_t)65536)
+clove_status_t clove_workspace_bind(void* ptr, size_t bytes);
+clove_status_t clove_workspace_query_begin(void);
+size_t clove_workspace_query_end(void);
 
 /* Frees the scratch buffers held for the current device (all streams),
  * including the SwiGLU intermediates and buffers replaced by larger ones.

@@ -46,7 +46,7 @@ def test_every_declared_symbol_is_exported(L):
 
 def test_status_strings_and_version(L):
     assert L.clove_abi_version() == 1
-    for code in range(8):
+    for code in range(9):
         assert L.clove_status_string(code).decode().startswith("CLOVE_")
     assert b"UNKNOWN" in L.clove_status_string(99)
 
