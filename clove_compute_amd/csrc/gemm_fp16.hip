@@ -71,18 +71,20 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
     const int nc = min(n, N - 8);
     const int kbeg = split * GV_ROWS;
 
-    u32x4 bv[GV_RPT];
-#pragma unroll
-    for (int j = 0; j < GV_RPT; ++j) {
-        const int k = min(kbeg + kl + GV_KL * j, K - 1);
-        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + (int64_t)k * N + nc));
-    }
+    // A (small, shared by every workgroup) first: loads complete in order, so
+    // the FMAs of row j wait only for B row j, not for the whole tile
     uint16_t xa[MM][GV_RPT];
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
         for (int j = 0; j < GV_RPT; ++j)
             xa[m][j] = A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + GV_KL * j, K - 1)];
+    u32x4 bv[GV_RPT];
+#pragma unroll
+    for (int j = 0; j < GV_RPT; ++j) {
+        const int k = min(kbeg + kl + GV_KL * j, K - 1);
+        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + (int64_t)k * N + nc));
+    }
 
     float acc[MM][8];
 #pragma unroll

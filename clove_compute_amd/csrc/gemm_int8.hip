@@ -332,18 +332,19 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
     const int nc = min(n, N - 16);
     const int kbeg = split * IV_ROWS;
 
-    u32x4 bv[IV_RPT];
-#pragma unroll
-    for (int j = 0; j < IV_RPT; ++j) {
-        const int k = min(kbeg + kl + IV_KL * j, K - 1);
-        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)k * N + nc));
-    }
+    // A first (see gemv_f16): the products of row j then wait only for B row j
     int8_t xa[MM][IV_RPT];
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
         for (int j = 0; j < IV_RPT; ++j)
             xa[m][j] = p.A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + IV_KL * j, K - 1)];
+    u32x4 bv[IV_RPT];
+#pragma unroll
+    for (int j = 0; j < IV_RPT; ++j) {
+        const int k = min(kbeg + kl + IV_KL * j, K - 1);
+        bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)k * N + nc));
+    }
 
     int acc[MM][16];
 #pragma unroll
