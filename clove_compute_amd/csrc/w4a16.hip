@@ -257,7 +257,13 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl == 2) g = {4, 2, 16};
     else g = {8, 1, 16};
     while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
-    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < cus) { g.rpw >>= 1; g.upr <<= 1; }
+    // one chunk per lane per row (K <= 2048): the loads in flight come from
+    // rows, so fewer rows per wave only adds workgroups; up to two per CU
+    // spreads the rows evenly (3072 rows: 768 workgroups, 3 per CU, rather
+    // than 384, some CUs holding twice the rows of others)
+    const int target = cpl == 1 ? 2 * cus : cus;
+    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < target) { g.rpw >>= 1; g.upr <<= 1; }
+    if (cpl == 1) g.upr = 1;
     if (g.upr > 8) g.upr = 8;
     return g;
 }
@@ -294,10 +300,13 @@ clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t 
         if (g.upr >= 8) return run_gemv_shape<TV, 1, 8>(p, g.wpb, aligned, stream);
         if (g.upr >= 6) return run_gemv_shape<TV, 1, 6>(p, g.wpb, aligned, stream);
         if (g.upr >= 4) return run_gemv_shape<TV, 1, 4>(p, g.wpb, aligned, stream);
-        return run_gemv_shape<TV, 1, 2>(p, g.wpb, aligned, stream);
+        if (g.upr >= 2) return run_gemv_shape<TV, 1, 2>(p, g.wpb, aligned, stream);
+        return run_gemv_shape<TV, 1, 1>(p, g.wpb, aligned, stream);
     }
-    if (g.rpw == 2) return run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return run_gemv_shape<TV, 4, 2>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr == 1 ? run_gemv_shape<TV, 2, 1>(p, g.wpb, aligned, stream)
+                                      : run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1>(p, g.wpb, aligned, stream)
+                                      : run_gemv_shape<TV, 4, 2>(p, g.wpb, aligned, stream);
     return run_gemv_shape<TV, 8, 1>(p, g.wpb, aligned, stream);
 }
 
