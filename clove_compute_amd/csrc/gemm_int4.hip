@@ -343,7 +343,11 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl == 2) g = {2, 2, 8};
     else g = {8, 1, 16};
     while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
-    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < cus) { g.rpw >>= 1; g.upr <<= 1; }
+    // one chunk per lane per row (K <= 2048): up to two workgroups per CU and
+    // one chunk load per row, as for the W4A16 GEMV (w4a16.hip)
+    const int target = cpl == 1 ? 2 * cus : cus;
+    while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < target) { g.rpw >>= 1; g.upr <<= 1; }
+    if (cpl == 1) g.upr = 1;
     if (g.upr > 8) g.upr = 8;
     return g;
 }
@@ -370,11 +374,14 @@ clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t 
         if (g.upr >= 8) return run_gemv_shape<NV, MODE, 1, 8>(p, g.wpb, aligned, stream);
         if (g.upr >= 6) return run_gemv_shape<NV, MODE, 1, 6>(p, g.wpb, aligned, stream);
         if (g.upr >= 4) return run_gemv_shape<NV, MODE, 1, 4>(p, g.wpb, aligned, stream);
-        return run_gemv_shape<NV, MODE, 1, 2>(p, g.wpb, aligned, stream);
+        if (g.upr >= 2) return run_gemv_shape<NV, MODE, 1, 2>(p, g.wpb, aligned, stream);
+        return run_gemv_shape<NV, MODE, 1, 1>(p, g.wpb, aligned, stream);
     }
-    if (g.rpw == 2) return g.upr >= 4 ? run_gemv_shape<NV, MODE, 2, 4>(p, g.wpb, aligned, stream)
-                              : run_gemv_shape<NV, MODE, 2, 2>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return run_gemv_shape<NV, MODE, 4, 2>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr >= 4   ? run_gemv_shape<NV, MODE, 2, 4>(p, g.wpb, aligned, stream)
+                           : g.upr >= 2 ? run_gemv_shape<NV, MODE, 2, 2>(p, g.wpb, aligned, stream)
+                                        : run_gemv_shape<NV, MODE, 2, 1>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return g.upr >= 2 ? run_gemv_shape<NV, MODE, 4, 2>(p, g.wpb, aligned, stream)
+                                      : run_gemv_shape<NV, MODE, 4, 1>(p, g.wpb, aligned, stream);
     return run_gemv_shape<NV, MODE, 8, 1>(p, g.wpb, aligned, stream);
 }
 
