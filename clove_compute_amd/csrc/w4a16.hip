@@ -257,13 +257,13 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl == 2) g = {4, 2, 16};
     else g = {8, 1, 16};
     while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
-    // one chunk per lane per row (K <= 2048): the loads in flight come from
-    // rows, so fewer rows per wave only adds workgroups; up to two per CU
-    // spreads the rows evenly (3072 rows: 768 workgroups, 3 per CU, rather
-    // than 384, some CUs holding twice the rows of others)
-    const int target = cpl == 1 ? 2 * cus : cus;
+    // fewer rows per wave, up to two workgroups per CU: the rows spread over
+    // the CUs evenly (3072 rows at K = 2048: 768 workgroups, 3 per CU, rather
+    // than 384, some CUs holding twice the rows of others); a lane never
+    // loads more chunks per row than the row has
+    const int target = 2 * cus;
     while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < target) { g.rpw >>= 1; g.upr <<= 1; }
-    if (cpl == 1) g.upr = 1;
+    if (g.upr > cpl) g.upr = cpl == 3 ? 4 : cpl;
     if (g.upr > 8) g.upr = 8;
     return g;
 }
