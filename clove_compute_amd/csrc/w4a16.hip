@@ -288,7 +288,8 @@ template <int TV>
 clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
     const GemvShape g = gemv_shape(2 * p.O, p.nch, cus);
     if (g.rpw <= 2) return run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return run_gemv_shape<TV, 4, 2, true>(p, g.wpb, aligned, stream);
+    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1, true>(p, g.wpb, aligned, stream)
+                                      : run_gemv_shape<TV, 4, 2, true>(p, g.wpb, aligned, stream);
     return run_gemv_shape<TV, 8, 1, true>(p, g.wpb, aligned, stream);
 }
 
