@@ -347,7 +347,9 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     // one chunk load per row, as for the W4A16 GEMV (w4a16.hip)
     const int target = cpl == 1 ? 2 * cus : cus;
     while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < target) { g.rpw >>= 1; g.upr <<= 1; }
-    if (cpl == 1) g.upr = 1;
+    // a lane never loads more chunks per row than the row has (rounded up to an
+    // instantiated width: 1, 2, 4, 6, 8)
+    if (g.upr > cpl) g.upr = cpl <= 2 ? cpl : cpl <= 4 ? 4 : cpl <= 6 ? 6 : 8;
     if (g.upr > 8) g.upr = 8;
     return g;
 }

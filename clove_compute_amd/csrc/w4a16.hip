@@ -263,7 +263,8 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     // loads more chunks per row than the row has
     const int target = 2 * cus;
     while (g.rpw > 1 && cdiv(rows, g.wpb * g.rpw) < target) { g.rpw >>= 1; g.upr <<= 1; }
-    if (g.upr > cpl) g.upr = cpl == 3 ? 4 : cpl;
+    // (rounded up to an instantiated width: 1, 2, 4, 6, 8)
+    if (g.upr > cpl) g.upr = cpl <= 2 ? cpl : cpl <= 4 ? 4 : cpl <= 6 ? 6 : 8;
     if (g.upr > 8) g.upr = 8;
     return g;
 }
