@@ -12,13 +12,18 @@ The same JSON line also carries:
   roofline      the headline kernel against MI355X dense FP16 MFMA peak, with
                 the HBM traffic per launch from the committed rocprof counters
   cpu_baseline  the oracle's restatement of the reference's naive GEMM
-                (fp32 sequential-k FMA), single thread, on a bounded row sample
+                (fp32 sequential-k FMA) on a bounded row sample: all usable
+                cores (`value`, `cores`) and one thread (`value_1_thread`),
+                with the host's nproc and CPU model
   shapes        every other shape of the five named configurations: FP16 512^3
                 and M = 1/32/128 at 4096x4096, INT8 M = 1/128, INT4 W4A4
                 (11008x4096 and 4096x11008, N = 1/16/128), the W4A16 Llama-1B
                 layer at T = 1 and 512 as the reference runtime sequences it and
-                with gate / up / SwiGLU fused; each with t_roof = max(flops / MFMA
-                peak, bytes / 8 TB/s) and frac_roofline = t_roof / time
+                with gate / up / SwiGLU fused, plus the reference benchmark's
+                other FP16 shapes (512x4096^2, 1x11008x4096, 1x4096x11008,
+                128x11008x4096, 128x4096x11008, 1024^3, 2048^3); each with
+                t_roof = max(flops / MFMA peak, bytes / 8 TB/s) and
+                frac_roofline = t_roof / time
 The shapes are timed as HIP-graph replays of one call per operand copy: the
 copies rotate through >= 512 MiB so that no call finds its weights in the
 256 MB Infinity Cache (cold), and the graph removes the per-call host launch
@@ -161,9 +166,34 @@ def compare_library(h, timer, steps, warmup, rounds=3):
     return out
 
 
+def cpu_threads():
+    """Threads for the all-cores CPU baseline: the cores this process may run
+    on, capped by OMP_NUM_THREADS when the host sets it (the GPU host's share of
+    its CPUs for one GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(h, seconds):
     """Times the oracle's naive-arithmetic FP16 GEMM on rows of the same
-    4096^3 problem, 64 rows at a time until `seconds` have passed."""
+    4096^3 problem: about half of `seconds` on one thread and half on all usable
+    cores (rows spread over POSIX threads).  Each leg is one call over a row
+    range sized from a short calibration, so B is widened to fp32 once per leg.
+    `value` is the all-cores figure."""
     import numpy as np
 
     import oracle
@@ -173,20 +203,35 @@ def cpu_baseline(h, seconds):
     M, K = A.shape
     N = B.shape[1]
     out = np.zeros((M, N), np.float16)
-    rows = 0
-    t0 = time.perf_counter()
-    while rows < M and time.perf_counter() - t0 < seconds:
-        r1 = min(M, rows + 64)
-        out[rows:r1] = oracle.gemm_fp16(A[rows:r1], B)
-        rows = r1
-    dt = time.perf_counter() - t0
+
+    def leg(r0, r1, nthreads):
+        t0 = time.perf_counter()
+        if nthreads == 1:
+            out[r0:r1] = oracle.gemm_fp16(A[r0:r1], B)
+        else:
+            out[r0:r1] = oracle.gemm_fp16_mt(A[r0:r1], B, (0, r1 - r0), nthreads)
+        return time.perf_counter() - t0
+
+    nt = cpu_threads()
+    # calibration on one thread: the difference of 12 and 4 rows leaves out
+    # the per-call widening of B
+    per_row = max((leg(0, 12, 1) - leg(0, 4, 1)) / 8, 1e-4)
+    rows1 = int(min(M // 2, max(8, seconds / 2 / per_row)))
+    dt1 = leg(0, rows1, 1)
+    rowsn = int(min(M - rows1, max(nt, seconds / 2 / (dt1 / rows1) * nt * 0.8)))
+    dtn = leg(rows1, rows1 + rowsn, nt)
+    tf1 = 2.0 * rows1 * N * K / dt1 / 1e12
+    tfn = 2.0 * rowsn * N * K / dtn / 1e12
     # the sampled rows double as a parity check of the timed GPU output
-    r8 = min(rows, 8)
-    ok, _ = within_tol(to_host(h["C"])[:r8], oracle.gemm_fp16_f64(A[:r8], B))
-    return dict(value=2.0 * rows * N * K / dt / 1e12, unit="TFLOP/s", cores=1, kind="port",
-                sample=f"rows 0..{rows - 1} of the 4096x4096x4096 FP16 GEMM ({rows} rows, "
-                       f"{dt:.1f} s), single thread, oracle/clove_oracle.c restatement of "
-                       f"gemm_fp16_naive_kernel",
+    done = rows1 + rowsn
+    pick = sorted({0, 1, rows1 - 1, rows1, done - 1})
+    ok, _ = within_tol(to_host(h["C"])[pick], oracle.gemm_fp16_f64(A[pick], B))
+    return dict(value=tfn, unit="TFLOP/s", cores=nt, kind="port",
+                value_1_thread=tf1, nproc=os.cpu_count(), cpu_model=cpu_model(),
+                sample=f"rows of the 4096x4096x4096 FP16 GEMM: rows 0..{rows1 - 1} on one thread "
+                       f"({rows1} rows, {dt1:.1f} s, {tf1 * 1e3:.2f} GFLOP/s), rows {rows1}..{done - 1} "
+                       f"on {nt} threads ({rowsn} rows, {dtn:.1f} s); oracle/clove_oracle.c restatement of "
+                       f"gemm_fp16_naive_kernel (fp32 sequential-k fmaf)",
                 parity_rows_ok=bool(ok))
 
 
@@ -275,6 +320,18 @@ def extras():
         calls = [lambda B=B, C=C, M=M: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
         record(f"fp16_{M}x4096x4096", calls, Cs, 2 * M * N * K, 2 * (M * K + K * N + M * N),
                PEAK_FP16_TFLOPS, hot_calls=calls[:1] * 16 if M == 1 else None)
+        del Bs, Cs, calls
+
+    # ---- the reference benchmark's other FP16 shapes (bench/bench_gemm.cu:20-37):
+    # (M, N, K) with activations ~N(0,1) and weights ~N(0,0.02), weights cold ----
+    for (M, N, K) in ((512, 4096, 4096), (1, 11008, 4096), (1, 4096, 11008), (128, 11008, 4096),
+                      (128, 4096, 11008), (1024, 1024, 1024), (2048, 2048, 2048)):
+        x = f16((M, K), 1.0, 40 + M)
+        Bs = [f16((K, N), 0.02, 140 + i) for i in range(copies_for(K * N * 2))]
+        Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
+        calls = [lambda B=B, C=C, M=M, N=N, K=K: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
+        record(f"ref_bench_fp16_{M}x{N}x{K}", calls, Cs, 2 * M * N * K, 2 * (M * K + K * N + M * N),
+               PEAK_FP16_TFLOPS)
         del Bs, Cs, calls
 
     # ---- INT8 W8A8 with per-row / per-column fp16 scales ----
@@ -420,6 +477,7 @@ def main():
     if args.cpu_seconds > 0:
         cb = cpu_baseline(h, args.cpu_seconds)
         cb["value"] = round(cb["value"], 6)
+        cb["value_1_thread"] = round(cb["value_1_thread"], 6)
         line["cpu_baseline"] = cb
     else:
         line["cpu_baseline"] = None

@@ -4,9 +4,12 @@
 // reference header include/clove/kernels/gemm.cuh:41-101, with hipStream_t in
 // place of cudaStream_t.  Every call forwards to the C ABI in <clove/gemm_c.h>;
 // a non-OK status is reported the reference's way (include/clove/common.cuh:11-21):
-// print file:line and the error, then exit(EXIT_FAILURE).
+// print file:line and the error, then exit(EXIT_FAILURE).  <clove/common.h>
+// brings the rest of the reference's common header: CLOVE_CHECK_CUDA /
+// CLOVE_CHECK_LAST / CLOVE_SYNC_CHECK, cdiv, DType, dtype_size, CudaType.
 #pragma once
 
+#include <clove/common.h>
 #include <clove/gemm_c.h>
 
 #include <hip/hip_fp16.h>
@@ -18,11 +21,33 @@
 
 namespace clove {
 
+// include/clove/kernels/gemm.cuh:13-31: the FP16 GEMM's tile configuration,
+// same member names.  The values describe this library's large-shape FP16
+// kernel on gfx950: a 256x256x64 workgroup tile of four 64-wide waves, each
+// wave a 128x128 tile of 16x16x32 fp16 MFMAs (fp32 accumulation).  Nothing in
+// the library reads these; they are informational, as in the reference.
+struct GemmConfig {
+    static constexpr int BM = 256;  // workgroup tile M
+    static constexpr int BN = 256;  // workgroup tile N
+    static constexpr int BK = 64;   // workgroup tile K (one LDS stage)
+
+    static constexpr int WM = 128;  // wave tile M
+    static constexpr int WN = 128;  // wave tile N
+
+    static constexpr int TM = 8;    // MFMA tiles per wave along M (WM / WMMA_M)
+    static constexpr int TN = 8;    // MFMA tiles per wave along N (WN / WMMA_N)
+
+    static constexpr int NUM_THREADS = 256;  // 4 waves of 64 lanes
+
+    // matrix-core instruction shape (v_mfma_f32_16x16x32_f16); the reference
+    // names it after WMMA
+    static constexpr int WMMA_M = 16;
+    static constexpr int WMMA_N = 16;
+    static constexpr int WMMA_K = 32;
+};
+
 // include/clove/kernels/gemm.cuh:72
 constexpr int INT4_GROUP_SIZE = CLOVE_INT4_GROUP_SIZE;
-
-// include/clove/common.cuh:30-32
-constexpr int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 namespace detail {
 inline void check(clove_status_t status, const char* file, int line) {

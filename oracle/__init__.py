@@ -47,6 +47,7 @@ def lib():
             "oracle_f16_to_f32_array": ([P, P, I64], None),
             "oracle_gemm_fp16_rows": ([P, P, P, I, I, I, F, F, I, I], None),
             "oracle_gemm_fp16": ([P, P, P, I, I, I, F, F], None),
+            "oracle_gemm_fp16_rows_mt": ([P, P, P, I, I, I, F, F, I, I, I], I),
             "oracle_gemm_fp16_f64": ([P, P, P, P, I, I, I, D, D], None),
             "oracle_gemm_fp16_batched": ([P, P, P, I, I, I, I, F, F], None),
             "oracle_gemm_int8": ([P, P, P, P, I, I, I, F, ctypes.c_int8, F, ctypes.c_int8], None),
@@ -104,6 +105,22 @@ def gemm_fp16(A, B, C=None, alpha=1.0, beta=0.0, rows=None) -> np.ndarray:
     out = np.zeros((M, N), np.float16) if C is None else _c(C, np.float16).copy()
     m0, m1 = (0, M) if rows is None else rows
     lib().oracle_gemm_fp16_rows(_p(A), _p(B), _p(out), M, N, K, alpha, beta, m0, m1)
+    return out
+
+
+def gemm_fp16_mt(A, B, rows, nthreads, C=None, alpha=1.0, beta=0.0) -> np.ndarray:
+    """gemm_fp16 on rows ``(m0, m1)`` with the rows spread over ``nthreads``
+    POSIX threads (bit-identical to ``gemm_fp16``); other rows stay as in C."""
+    A = _c(A, np.float16)
+    B = _c(B, np.float16)
+    M, K = A.shape
+    K2, N = B.shape
+    assert K == K2
+    out = np.zeros((M, N), np.float16) if C is None else _c(C, np.float16).copy()
+    m0, m1 = rows
+    r = lib().oracle_gemm_fp16_rows_mt(_p(A), _p(B), _p(out), M, N, K, alpha, beta, m0, m1, nthreads)
+    if r < 0:
+        raise MemoryError("oracle_gemm_fp16_rows_mt")
     return out
 
 

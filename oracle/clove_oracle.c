@@ -6,6 +6,7 @@
 #include "clove_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -124,6 +125,68 @@ void oracle_gemm_fp16_rows(const uint16_t* A, const uint16_t* B, uint16_t* C,
 void oracle_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C,
                       int M, int N, int K, float alpha, float beta) {
     oracle_gemm_fp16_rows(A, B, C, M, N, K, alpha, beta, 0, M);
+}
+
+/* The same arithmetic as oracle_gemm_fp16_rows (per-element sequential k,
+ * fp32 fmaf, the same epilogue), rows [m0, m1) split over `nthreads` POSIX
+ * threads: thread t takes rows m0 + t, m0 + t + nthreads, ...  B is widened
+ * once and shared.  Each output element is computed by exactly one thread in
+ * the single-thread order, so the result is bit-identical to
+ * oracle_gemm_fp16_rows for any thread count. */
+struct fp16_mt_job {
+    const uint16_t* A;
+    const float* Bf;
+    uint16_t* C;
+    int N, K, m0, m1, t, nt;
+    float alpha, beta;
+};
+
+static void* fp16_mt_worker(void* arg) {
+    const struct fp16_mt_job* j = (const struct fp16_mt_job*)arg;
+    float* s = (float*)malloc((size_t)j->N * sizeof(float));
+    if (!s) return NULL;
+    for (int m = j->m0 + j->t; m < j->m1; m += j->nt) {
+        for (int n = 0; n < j->N; n++) s[n] = 0.0f;
+        const uint16_t* Arow = j->A + (int64_t)m * j->K;
+        for (int k = 0; k < j->K; k++) {
+            const float a = oracle_f16_to_f32(Arow[k]);
+            const float* Brow = j->Bf + (int64_t)k * j->N;
+            for (int n = 0; n < j->N; n++) s[n] = fmaf(a, Brow[n], s[n]);
+        }
+        uint16_t* Crow = j->C + (int64_t)m * j->N;
+        for (int n = 0; n < j->N; n++) {
+            float r = j->alpha * s[n];
+            if (j->beta != 0.0f) r = fmaf(j->beta, oracle_f16_to_f32(Crow[n]), r);
+            Crow[n] = oracle_f32_to_f16(r);
+        }
+    }
+    free(s);
+    return NULL;
+}
+
+int oracle_gemm_fp16_rows_mt(const uint16_t* A, const uint16_t* B, uint16_t* C,
+                             int M, int N, int K, float alpha, float beta,
+                             int m0, int m1, int nthreads) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    if (m0 < 0) m0 = 0;
+    if (m1 > M) m1 = M;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    float* Bf = widen(B, (int64_t)K * N);
+    if (!Bf) return -1;
+    pthread_t th[256];
+    struct fp16_mt_job jobs[256];
+    int started = 0;
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t] = (struct fp16_mt_job){A, Bf, C, N, K, m0, m1, t, nthreads, alpha, beta};
+        if (pthread_create(&th[t], NULL, fp16_mt_worker, &jobs[t]) != 0) break;
+        started++;
+    }
+    for (int t = 0; t < started; t++) pthread_join(th[t], NULL);
+    /* rows of threads that could not start: computed here, same order */
+    for (int t = started; t < nthreads; t++) fp16_mt_worker(&jobs[t]);
+    free(Bf);
+    return started;
 }
 
 void oracle_gemm_fp16_f64(const uint16_t* A, const uint16_t* B,

@@ -50,6 +50,13 @@ void oracle_gemm_fp16_rows(const uint16_t* A, const uint16_t* B, uint16_t* C,
                            int m0, int m1);
 void oracle_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C,
                       int M, int N, int K, float alpha, float beta);
+/* oracle_gemm_fp16_rows with the rows spread over `nthreads` POSIX threads
+ * (bit-identical to it: every element is one thread's sequential-k sum).
+ * Returns the number of threads started (the rest run on the caller), -1 if
+ * out of memory.  Used by the bench's all-cores CPU baseline. */
+int oracle_gemm_fp16_rows_mt(const uint16_t* A, const uint16_t* B, uint16_t* C,
+                             int M, int N, int K, float alpha, float beta,
+                             int m0, int m1, int nthreads);
 
 /* Unrounded float64 value of alpha * A @ B + beta * C_in (C_in may be NULL). */
 void oracle_gemm_fp16_f64(const uint16_t* A, const uint16_t* B,

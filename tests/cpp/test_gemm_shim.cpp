@@ -48,22 +48,30 @@ std::vector<uint16_t> rand_f16(size_t n, float lo, float hi, Rng& g) {
     return v;
 }
 
+// element type of a host vector, as the reference's Tensor records it
+// (src/runtime/tensor.cu:62-65 sizes a buffer as numel * dtype_size(dtype))
+template <class T> constexpr clove::DType dtype_of();
+template <> constexpr clove::DType dtype_of<uint16_t>() { return clove::DType::FP16; }
+template <> constexpr clove::DType dtype_of<int8_t>() { return clove::DType::INT8; }
+template <> constexpr clove::DType dtype_of<uint8_t>() { return clove::DType::INT8; }  // packed INT4 bytes
+
+// the reference's error convention around every runtime call
+// (include/clove/common.cuh:11-27)
 template <class T>
 T* to_dev(const std::vector<T>& h) {
+    static_assert(sizeof(T) == 1 || sizeof(T) == 2, "element size");
+    const size_t bytes = h.size() * clove::dtype_size(dtype_of<T>());
     T* d = nullptr;
-    if (hipMalloc(&d, h.size() * sizeof(T) + 16) != hipSuccess) {
-        std::fprintf(stderr, "hipMalloc failed\n");
-        std::exit(2);
-    }
-    (void)hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice);
+    CLOVE_CHECK_CUDA(hipMalloc(&d, bytes + 16));
+    CLOVE_CHECK_CUDA(hipMemcpy(d, h.data(), bytes, hipMemcpyHostToDevice));
     return d;
 }
 
 template <class T>
 std::vector<T> to_host(const T* d, size_t n) {
     std::vector<T> h(n);
-    (void)hipDeviceSynchronize();
-    (void)hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost);
+    CLOVE_SYNC_CHECK();
+    CLOVE_CHECK_CUDA(hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost));
     return h;
 }
 
@@ -108,6 +116,7 @@ void fp16_case(const char* name, int M, int N, int K, float alpha, float beta, u
     auto C0 = rand_f16((size_t)M * N, -1.0f, 1.0f, g);
     uint16_t *dA = to_dev(A), *dB = to_dev(B), *dC = to_dev(C0);
     clove::gemm_fp16(H(dA), H(dB), H(dC), M, N, K, alpha, beta);  // defaults: stream 0
+    CLOVE_CHECK_LAST();  // as the reference's launcher does after its kernel (gemm_fp16.cu:304)
     auto got = to_host(dC, (size_t)M * N);
     std::vector<double> ref((size_t)M * N);
     oracle_gemm_fp16_f64(A.data(), B.data(), beta != 0.0f ? C0.data() : nullptr, ref.data(), M, N, K, alpha, beta);
@@ -179,7 +188,7 @@ void int8_case(int M, int N, int K) {
 // ---- INT4: group-wise (tolerance) and the reference-literal mode (bit-exact) ----
 void int4_case(int M, int N, int K) {
     Rng g(41 + N);
-    const int G = (K + 127) / 128, ldb = (N + 1) / 2;
+    const int G = clove::cdiv(K, clove::INT4_GROUP_SIZE), ldb = clove::cdiv(N, 2);
     std::vector<uint8_t> A((size_t)M * (K / 2)), B((size_t)K * ldb);
     for (auto& x : A) x = (uint8_t)g.integer(0, 255);
     for (auto& x : B) x = (uint8_t)g.integer(0, 255);
@@ -225,7 +234,7 @@ void w4a16_mlp_case(int T) {
     const int H_ = 256, I = 384;  // hidden, intermediate
     Rng g(51 + T);
     auto X = rand_f16((size_t)T * H_, -1.0f, 1.0f, g);
-    const int Gh = H_ / 128, Gi = I / 128;
+    const int Gh = clove::cdiv(H_, clove::INT4_GROUP_SIZE), Gi = clove::cdiv(I, clove::INT4_GROUP_SIZE);
     std::vector<uint8_t> Wgu((size_t)2 * I * (H_ / 2)), Wd((size_t)H_ * (I / 2));
     for (auto& x : Wgu) x = (uint8_t)g.integer(0, 255);
     for (auto& x : Wd) x = (uint8_t)g.integer(0, 255);
@@ -294,6 +303,19 @@ int main() {
         return 2;
     }
     std::printf("clove C ABI version %d\n", clove_abi_version());
+    // the reference header's types and constants, as its callers spell them
+    static_assert(clove::CudaType<half>::dtype == clove::DType::FP16, "CudaType<half>");
+    static_assert(clove::GemmConfig::NUM_THREADS == 64 * (clove::GemmConfig::BM / clove::GemmConfig::WM) *
+                                                        (clove::GemmConfig::BN / clove::GemmConfig::WN),
+                  "GemmConfig: one 64-lane wave per wave tile");
+    if (clove::dtype_size(clove::DType::FP32) != 4 || clove::dtype_size(clove::DType::FP16) != 2 ||
+        clove::dtype_size(clove::DType::BF16) != 2 || clove::dtype_size(clove::DType::INT8) != 1 ||
+        clove::dtype_size(clove::DType::INT4) != 0) {
+        std::printf("dtype_size FAIL\n");
+        ++g_failed;
+    }
+    std::printf("GemmConfig %dx%dx%d, %d threads\n", clove::GemmConfig::BM, clove::GemmConfig::BN,
+                clove::GemmConfig::BK, clove::GemmConfig::NUM_THREADS);
     fp16_case("test_gemm_small 64^3", 64, 64, 64, 1.0f, 0.0f, 1);
     fp16_case("test_gemm_medium 256^3", 256, 256, 256, 1.0f, 0.0f, 2);
     fp16_case("test_gemm_large 1024^3", 1024, 1024, 1024, 1.0f, 0.0f, 3);

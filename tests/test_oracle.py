@@ -132,6 +132,24 @@ def test_fp16_row_range_only_touches_rows():
     assert np.all(C[:2] == 7.0) and np.all(C[5:] == 7.0)
 
 
+@pytest.mark.parametrize("nthreads", [1, 3, 8])
+def test_fp16_threaded_rows_equal_single_thread(nthreads):
+    # the all-cores CPU baseline: rows spread over threads, same bits as one
+    # thread (random fp16 operands, so the order of every sum matters), rows
+    # outside the range untouched
+    A = RNG.standard_normal((13, 96)).astype(np.float16)
+    B = RNG.standard_normal((96, 40)).astype(np.float16)
+    C0 = RNG.standard_normal((13, 40)).astype(np.float16)
+    ref = oracle.gemm_fp16(A, B, C0, alpha=0.5, beta=0.25, rows=(2, 11))
+    got = oracle.gemm_fp16_mt(A, B, (2, 11), nthreads, C0, alpha=0.5, beta=0.25)
+    assert np.array_equal(f16bits(got), f16bits(ref))
+    assert np.array_equal(f16bits(got[:2]), f16bits(C0[:2]))
+    assert np.array_equal(f16bits(got[11:]), f16bits(C0[11:]))
+    # and against the float64 closed form within the forward-error bound
+    f64 = oracle.gemm_fp16_f64(A[2:11], B, C0[2:11], 0.5, 0.25)
+    assert np.all(np.abs(got[2:11].astype(np.float64) - f64) <= 1e-2 * np.maximum(np.abs(f64), 1e-1))
+
+
 def test_fp16_batched_matches_per_batch():
     A = RNG.integers(-4, 5, (3, 10, 20)).astype(np.float16)
     B = RNG.integers(-4, 5, (3, 20, 12)).astype(np.float16)
