@@ -19,7 +19,8 @@ The same JSON line also carries:
                 and M = 1/32/128 at 4096x4096, INT8 M = 1/128, INT4 W4A4
                 (11008x4096 and 4096x11008, N = 1/16/128), the W4A16 Llama-1B
                 layer at T = 1 and 512 as the reference runtime sequences it and
-                with gate / up / SwiGLU fused, plus the reference benchmark's
+                with gate / up / SwiGLU fused, the FP16 Llama-1B MLP gate / up +
+                SwiGLU (swiglu_fused) at T = 1 and 512, plus the reference benchmark's
                 other FP16 shapes (512x4096^2, 1x11008x4096, 1x4096x11008,
                 128x11008x4096, 128x4096x11008, 1024^3, 2048^3); each with
                 t_roof = max(flops / MFMA peak, bytes / 8 TB/s) and
@@ -421,6 +422,31 @@ def extras():
         record(f"w4a16_llama1b_layer_fused_T{T}", calls, [q, h], flops, wbytes + lin_f,
                PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3)
         del fused, calls
+
+    # ---- FP16 Llama-1B MLP: gate / up projections and SwiGLU on FP16 weights
+    # [2048, 8192] (the reference's declared swiglu_fused), one fused launch,
+    # and the same as two gemm_fp16 calls and swiglu for comparison ----
+    H, I = 2048, 8192
+    wb = 2 * H * I * 2
+    for T in (1, 512):
+        x = f16((T, H), 1.0, 950)
+        pairs = [(f16((H, I), 0.02, 960 + 2 * i), f16((H, I), 0.02, 961 + 2 * i)) for i in range(copies_for(wb))]
+        outs = [torch.empty(T, I, dtype=torch.float16, device="cuda") for _ in pairs]
+        flops = 2 * 2 * T * H * I
+        calls = [lambda w=w, o=o, T=T: cg.swiglu_fused(x, w[0], w[1], o, T, H, I) for w, o in zip(pairs, outs)]
+        record(f"fp16_llama1b_mlp_swiglu_fused_T{T}", calls, outs, flops, wb + 2 * T * H + 2 * T * I,
+               PEAK_FP16_TFLOPS)
+        gate = torch.empty(T, I, dtype=torch.float16, device="cuda")
+        up = torch.empty_like(gate)
+
+        def unfused(w, o, T=T):
+            cg.gemm_fp16(x, w[0], gate, T, I, H)
+            cg.gemm_fp16(x, w[1], up, T, I, H)
+            cg.swiglu(gate, up, o, T * I)
+        calls = [lambda w=w, o=o: unfused(w, o) for w, o in zip(pairs, outs)]
+        record(f"fp16_llama1b_mlp_unfused_T{T}", calls, outs, flops,
+               wb + 2 * 2 * T * H + 3 * 2 * 2 * T * I, PEAK_FP16_TFLOPS)
+        del pairs, outs, calls
     return out
 
 

@@ -2,7 +2,9 @@
 
 Each .hip source under csrc/ is compiled to an object for gfx950 only, then
 linked into clove_compute_amd/lib/libclove_gemm.so.  Objects are rebuilt when
-their source or any header is newer (force=True rebuilds everything).
+their source or any header is newer (force=True rebuilds everything).  The
+build then reads every kernel's register and scratch use from the code objects
+(resources.py) and fails if a kernel outside the unaligned fallbacks spills.
 """
 from __future__ import annotations
 
@@ -75,6 +77,9 @@ def build(force: bool = False, jobs: int = 8) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libclove_gemm.so failed")
     os.replace(LIB + ".tmp", LIB)
+    # no kernel that an aligned call can reach may spill registers to scratch
+    from clove_compute_amd import resources
+    resources.check(objs)
     return LIB
 
 

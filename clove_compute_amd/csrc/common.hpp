@@ -60,6 +60,39 @@ __device__ __forceinline__ uint16_t swiglu_h(uint16_t g, uint16_t u) {
     return f2h(s * h2f(u));
 }
 
+// ---------------------------------------------------------------------------
+// Cross-lane sums without the LDS pipe: gfx950's v_permlane16_swap /
+// v_permlane32_swap exchange 16-lane rows (or 32-lane halves) between two
+// registers in the VALU.  With the rows of a wave r0..r3:
+//   permlane16_swap(x, y) -> {[x0 y0 x2 y2], [x1 y1 x3 y3]}
+//   permlane32_swap(x, y) -> {[x0 x1 y0 y1], [x2 x3 y2 y3]}
+// so adding the two results sums two registers across the swapped lanes at
+// once, each in its own half of the wave.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T swap_sum16(T x, T y) {
+    const auto s = __builtin_amdgcn_permlane16_swap(bitcast<unsigned>(x), bitcast<unsigned>(y), false, false);
+    return bitcast<T>(s[0]) + bitcast<T>(s[1]);
+}
+template <typename T>
+__device__ __forceinline__ T swap_sum32(T x, T y) {
+    const auto s = __builtin_amdgcn_permlane32_swap(bitcast<unsigned>(x), bitcast<unsigned>(y), false, false);
+    return bitcast<T>(s[0]) + bitcast<T>(s[1]);
+}
+// Four registers summed over the four lanes l, l^16, l^32, l^48: lane l of
+// row r returns the sum of v[r], added as (row 0 + row 1) + (row 2 + row 3)
+// -- the order of an xor-16 then xor-32 butterfly.
+template <typename T>
+__device__ __forceinline__ T rows_sum4(T v0, T v1, T v2, T v3) {
+    return swap_sum32(swap_sum16(v0, v1), swap_sum16(v2, v3));
+}
+// Two registers summed over lanes l and l^32: lanes 0..31 return the sum of
+// x, lanes 32..63 that of y, each as (lane l) + (lane l + 32).
+template <typename T>
+__device__ __forceinline__ T halves_sum2(T x, T y) {
+    return swap_sum32(x, y);
+}
+
 // Streaming GEMVs with V weight columns (or token rows): the wide variants
 // (V >= WIDE) and the byte-gathering unaligned ones need more than the 128
 // VGPRs a 1024-thread workgroup leaves, so they run with at most 512 threads

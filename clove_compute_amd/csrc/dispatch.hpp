@@ -122,6 +122,16 @@ constexpr int kBufSwiglu = 1;  // gate / up intermediates of the unfused SwiGLU 
 bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N, int K,
                      float alpha, float beta, int num_cus, hipStream_t stream, clove_status_t* status);
 bool try_skinny_int8(const Int8Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+// out [T, inter] = swiglu(fp16(X @ W_gate), fp16(X @ W_up)) in one pass of the
+// skinny kernel with two B operands (T > 4, aligned, hidden % 64 == 0); same
+// tiles and split plan as try_skinny_fp16 picks for each projection
+bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
+                       int hidden, int inter, int num_cus, hipStream_t stream, clove_status_t* status);
+// the same for T <= 4 on the FP16 GEMV (gemm_fp16.hip): each workgroup streams
+// 128 columns of W_gate and the same 128 columns of W_up; false when the
+// operands are not 16-byte aligned or hidden / inter are not multiples of 8
+bool try_gemv_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
+                     int hidden, int inter, hipStream_t stream, clove_status_t* status);
 
 inline clove_status_t check_launch() {
     return hipGetLastError() == hipSuccess ? CLOVE_OK : CLOVE_ERR_LAUNCH;

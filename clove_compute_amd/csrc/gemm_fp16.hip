@@ -29,14 +29,15 @@ using namespace hw;
 // 16 bytes of columns 8cl..8cl+7 of rows kl + 32j, j < 8, so each wave
 // instruction reads two full 512-byte row segments and the whole 128 KB tile is
 // requested at once.  Loads are unconditional from clamped addresses (masked
-// at use).  Partials: wave halves, then the 16 waves through LDS (fixed
-// order), then the K splits, summed by the last workgroup to arrive (coherent
-// stores and loads, split order).
+// at use).  Partials: wave halves (v_permlane32_swap), then the 16 waves
+// through LDS (fixed order), then the K splits, summed by the last workgroup
+// to arrive (coherent stores and loads, split order).
 // ---------------------------------------------------------------------------
 struct GemvParams {
     const uint16_t* A;
     const uint16_t* B;
     uint16_t* C;
+    const uint16_t* B2;  // SWIGLU: the up projection's weights (B holds the gate's)
     int M, N, K;
     float alpha, beta;
     int64_t strideA, strideB, strideC;
@@ -51,10 +52,18 @@ constexpr int GV_KL = 32;                 // k lanes
 constexpr int GV_RPT = 8;                 // rows per thread
 constexpr int GV_ROWS = GV_KL * GV_RPT;   // k rows per workgroup
 
-template <int MM>
+// SWIGLU: the workgroup's 256 columns are 128 columns of B (gate) and the
+// same 128 columns of B2 (up): column lanes 0..15 read B, 16..31 read B2, so a
+// wave instruction reads two 256-byte row segments.  Every column's sum runs
+// over the same k in the same order as in the one-operand kernel (the k
+// mapping does not depend on the column), so gate and up are bit-identical
+// to two gemm_fp16 calls; the epilogue rounds both to fp16 and applies SwiGLU.
+template <int MM, bool SWIGLU = false>
 __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
     __shared__ float red[16][MM][GV_COLS];
+    __shared__ float s_up[SWIGLU ? MM : 1][SWIGLU ? GV_COLS / 2 : 1];
     __shared__ int s_last;
+    constexpr int CW = SWIGLU ? GV_COLS / 2 : GV_COLS;  // output columns per workgroup
     const int tid = threadIdx.x;
     const int cl = tid & 31, kl = tid >> 5, wave = tid >> 6;
     int bid = blockIdx.x;
@@ -63,11 +72,10 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
     const int batch = bid / p.col_blocks;
     const int cb = bid - batch * p.col_blocks;
     const uint16_t* __restrict__ A = p.A + batch * p.strideA;
-    const uint16_t* __restrict__ B = p.B + batch * p.strideB;
+    const uint16_t* __restrict__ B = (SWIGLU && cl >= 16 ? p.B2 : p.B) + batch * p.strideB;
     uint16_t* __restrict__ C = p.C + batch * p.strideC;
     const int M = p.M, N = p.N, K = p.K;
-    const int n = cb * GV_COLS + cl * 8;
-    const bool col_ok = n < N;
+    const int n = cb * CW + (SWIGLU ? cl & 15 : cl) * 8;
     const int nc = min(n, N - 8);
     const int kbeg = split * GV_ROWS;
 
@@ -106,17 +114,14 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
             for (int e = 0; e < 8; ++e) acc[m][e] = fmaf(a, bf[e], acc[m][e]);
         }
     }
-    // the two k lanes of a wave (lanes l and l + 32), then the 16 waves
+    // the two k lanes of a wave (lanes l and l + 32, summed in that order) by
+    // a half-wave swap: lanes 0..31 keep the even columns of their 8, lanes
+    // 32..63 the odd ones; then the 16 waves through LDS
+    const int half = (tid >> 5) & 1;
 #pragma unroll
     for (int m = 0; m < MM; ++m)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[m][e] += __shfl_xor(acc[m][e], 32);
-    if ((tid & 32) == 0) {
-#pragma unroll
-        for (int m = 0; m < MM; ++m)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) red[wave][m][cl * 8 + e] = acc[m][e];
-    }
+        for (int e = 0; e < 8; e += 2) red[wave][m][cl * 8 + e + half] = halves_sum2(acc[m][e], acc[m][e + 1]);
     __syncthreads();
     // threads 0..255 own one column each from here on; every thread still
     // takes part in the arrival barrier
@@ -162,6 +167,22 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
 #pragma unroll
                 for (int m = 0; m < MM; ++m) sum[m] += part[s][m];
         }
+    }
+    if constexpr (SWIGLU) {
+        // columns 128..255 of the workgroup are the up sums of columns 0..127
+        if (active && tid >= CW) {
+#pragma unroll
+            for (int m = 0; m < MM; ++m) s_up[m][tid - CW] = sum[m];
+        }
+        __syncthreads();
+        if (tid >= CW) return;
+        const int go = cb * CW + tid;
+        if (go < N) {
+#pragma unroll
+            for (int m = 0; m < MM; ++m)
+                if (m < M) C[(int64_t)m * N + go] = swiglu_h(f2h(sum[m]), f2h(s_up[m][tid]));
+        }
+        return;
     }
     if (!active) return;
     if (gn < N) {
@@ -242,9 +263,9 @@ clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int ba
     return check_launch();
 }
 
-template <int MM>
+template <int MM, bool SWIGLU = false>
 clove_status_t run_gemv(GemvParams p, int batch, hipStream_t stream) {
-    p.col_blocks = cdiv(p.N, GV_COLS);
+    p.col_blocks = cdiv(p.N, SWIGLU ? GV_COLS / 2 : GV_COLS);
     p.nsplit = cdiv(p.K, GV_ROWS);
     const int tiles = p.col_blocks * batch;
     p.ws = nullptr;
@@ -259,12 +280,25 @@ clove_status_t run_gemv(GemvParams p, int batch, hipStream_t stream) {
     }
     const int64_t grid = (int64_t)tiles * p.nsplit;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
-    CLOVE_LAUNCH((gemv_f16<MM>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
+    CLOVE_LAUNCH((gemv_f16<MM, SWIGLU>), dim3((unsigned)grid), dim3(1024), 0, stream, p);
     return check_launch();
 }
 
 }  // namespace
 }  // namespace fp16
+
+bool try_gemv_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
+                     int hidden, int inter, hipStream_t stream, clove_status_t* status) {
+    using namespace fp16;
+    if (T < 1 || T > 4 || hidden <= 0 || hidden % 8 != 0 || inter < 8 || inter % 8 != 0) return false;
+    if (!aligned16(X) || !aligned16(W_gate) || !aligned16(W_up) || !aligned16(out)) return false;
+    const int64_t sA = (int64_t)T * hidden, sB = (int64_t)hidden * inter, sC = (int64_t)T * inter;
+    GemvParams g{X, W_gate, out, W_up, T, inter, hidden, 1.0f, 0.0f, sA, sB, sC, 0, 1, nullptr, nullptr};
+    if (T == 1) *status = run_gemv<1, true>(g, 1, stream);
+    else if (T == 2) *status = run_gemv<2, true>(g, 1, stream);
+    else *status = run_gemv<4, true>(g, 1, stream);
+    return true;
+}
 
 clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch,
                                 int M, int N, int K, float alpha, float beta,
@@ -278,7 +312,7 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
     const int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
 
     if (aligned && M <= 4 && K > 0) {
-        GemvParams g{A, B, C, M, N, K, alpha, beta, sA, sB, sC, 0, 1, nullptr, nullptr};
+        GemvParams g{A, B, C, nullptr, M, N, K, alpha, beta, sA, sB, sC, 0, 1, nullptr, nullptr};
         if (M == 1) return run_gemv<1>(g, batch, stream);
         if (M == 2) return run_gemv<2>(g, batch, stream);
         return run_gemv<4>(g, batch, stream);
@@ -297,7 +331,6 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
         if (try_skinny_fp16(A, B, C, batch, M, N, K, alpha, beta, cus, stream, &st2)) return st2;
     }
     if (aligned) {
-        if (big_tiles >= cus / 2) return run_mfma<Tile<256, 256, 64, 2, 2>, true>(p, batch, cus, stream);
         if (M <= 32) return run_mfma<Tile<32, 128, 64, 1, 4>, true>(p, batch, cus, stream);
         if (M <= 64) return run_mfma<Tile<64, 128, 64, 2, 2>, true>(p, batch, cus, stream);
         if (M <= 192) return run_mfma<Tile<128, 64, 128, 2, 2>, true>(p, batch, cus, stream);

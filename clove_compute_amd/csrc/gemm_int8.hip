@@ -313,19 +313,26 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
 // row segments and the whole 128 KB tile is requested at once (4096 x 4096:
 // 9.8 us with 256-row tiles, 9.2 with 512, 11.8 with 1024, measured).  Loads are
 // unconditional from clamped addresses (masked at use).  int32 partials:
-// within a wave (4 k lanes), across the 16 waves through LDS, then across the
-// K splits by the last workgroup to arrive (split order).
+// within a wave (4 k lanes, by v_permlane row swaps), across the 16 waves
+// through LDS, then across the K splits by the last workgroup to arrive
+// (split order).
+// With 4 output rows the accumulators (64) and 8 rows of B in flight (32)
+// exceed the 128 VGPRs of a 1024-thread workgroup, so MM = 4 takes 4 rows per
+// thread (a 256-row tile, twice the K splits) and runs without scratch.
 constexpr int IV_COLS = 256;
 constexpr int IV_KL = 64;
-constexpr int IV_RPT = 8;
-constexpr int IV_ROWS = IV_KL * IV_RPT;
+template <int MM>
+constexpr int iv_rpt() { return MM >= 4 ? 4 : 8; }
+template <int MM>
+constexpr int iv_rows() { return IV_KL * iv_rpt<MM>(); }
 
 template <int MM, int OUT>
 __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
+    constexpr int IV_RPT = iv_rpt<MM>(), IV_ROWS = iv_rows<MM>();
     __shared__ int red[16][MM][IV_COLS];
     __shared__ int s_last;
     const int tid = threadIdx.x;
-    const int cl = tid & 15, kl = tid >> 4, wave = tid >> 6;
+    const int cl = tid & 15, kl = tid >> 4, wave = tid >> 6, lane = tid & 63;
     const int split = blockIdx.x % p.nsplit;
     const int cb = blockIdx.x / p.nsplit;
     const int M = p.M, N = p.N, K = p.K;
@@ -347,39 +354,40 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
         bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)k * N + nc));
     }
 
-    int acc[MM][16];
+    // Rows of A in passes of at most two (B stays in registers): the 16 column
+    // accumulators of four rows would not fit beside the loads in flight.
+    constexpr int MC = MM >= 4 ? 2 : MM;
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
+    for (int m0 = 0; m0 < MM; m0 += MC) {
+        int acc[MC][16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[m][e] = 0;
+        for (int m = 0; m < MC; ++m)
 #pragma unroll
-    for (int j = 0; j < IV_RPT; ++j) {
-        const bool row_ok = kbeg + kl + IV_KL * j < K;
-        int bvals[16];
-        const unsigned w[4] = {bv[j].x, bv[j].y, bv[j].z, bv[j].w};
+            for (int e = 0; e < 16; ++e) acc[m][e] = 0;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) bvals[e] = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
-#pragma unroll
-        for (int m = 0; m < MM; ++m) {
+        for (int j = 0; j < IV_RPT; ++j) {
+            const bool row_ok = kbeg + kl + IV_KL * j < K;
+            const unsigned w[4] = {bv[j].x, bv[j].y, bv[j].z, bv[j].w};
             // |a - za|, |b - zb| <= 255: 24-bit products are exact
-            const int a = (row_ok && m < M) ? (int)xa[m][j] - p.za : 0;
+            int a[MC];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[m][e] += __mul24(a, bvals[e]);
+            for (int m = 0; m < MC; ++m) a[m] = (row_ok && m0 + m < M) ? (int)xa[m0 + m][j] - p.za : 0;
+            // each byte of B is extracted once and used for every row
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int b = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
+#pragma unroll
+                for (int m = 0; m < MC; ++m) acc[m][e] += __mul24(a[m], b);
+            }
         }
-    }
-    // the four k lanes of a wave (lanes l, l+16, l+32, l+48), then the 16 waves
+        // the four k lanes of a column lane (l, l+16, l+32, l+48) by row
+        // swaps: lane l of row r ends with column 16 cl + 4 u + r, u < 4
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
+        for (int m = 0; m < MC; ++m)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            acc[m][e] += __shfl_xor(acc[m][e], 16);
-            acc[m][e] += __shfl_xor(acc[m][e], 32);
-        }
-    if ((tid & 48) == 0) {
-#pragma unroll
-        for (int m = 0; m < MM; ++m)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) red[wave][m][cl * 16 + e] = acc[m][e];
+            for (int u = 0; u < 4; ++u)
+                red[wave][m0 + m][cl * 16 + 4 * u + (lane >> 4)] =
+                    rows_sum4(acc[m][4 * u], acc[m][4 * u + 1], acc[m][4 * u + 2], acc[m][4 * u + 3]);
     }
     __syncthreads();
     // threads 0..255 own one column each from here on; every thread still
@@ -405,21 +413,23 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
         if (!splitk_arrive_is_last(&p.counters[cb], (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
         for (int m = 0; m < MM; ++m) sum[m] = 0;
-        for (int s0 = 0; s0 < p.nsplit; s0 += 16) {
-            int part[16][MM];
+        // partials in flight together: 64 registers' worth
+        constexpr int SB = 64 / MM;
+        for (int s0 = 0; s0 < p.nsplit; s0 += SB) {
+            int part[SB][MM];
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
+            for (int s = 0; s < SB; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
                     part[s][m] = __float_as_int(load_coherent(
                         &ws_tile[(int64_t)min(s0 + s, p.nsplit - 1) * MM * IV_COLS + m * IV_COLS + col]));
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
+            for (int s = 0; s < SB; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
                     if (s0 + s >= p.nsplit) part[s][m] = 0;
 #pragma unroll
-            for (int s = 0; s < 16; ++s)
+            for (int s = 0; s < SB; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m) sum[m] += part[s][m];
         }
@@ -445,11 +455,12 @@ namespace {
 template <int OUT>
 clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     const int col_blocks = cdiv(p.N, IV_COLS);
-    p.nsplit = cdiv(p.K, IV_ROWS);
-    p.k_per_split = IV_ROWS;
+    const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
+    const int rows = mm == 1 ? iv_rows<1>() : (mm == 2 ? iv_rows<2>() : iv_rows<4>());
+    p.nsplit = cdiv(p.K, rows);
+    p.k_per_split = rows;
     if (p.nsplit > 1) {
         Scratch s;
-        const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
         clove_status_t st = acquire_scratch(stream, (size_t)col_blocks * p.nsplit * mm * IV_COLS * 4,
                                             (size_t)col_blocks, &s);
         if (st != CLOVE_OK) return st;

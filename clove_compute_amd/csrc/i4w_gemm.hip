@@ -109,15 +109,18 @@ clove_status_t launch_stream(const Args& a, hipStream_t stream) {
 
 // K slices: the fewest waves (2, 4 or 8) that leave each at most 11 groups,
 // unrolled for 8 groups when that suffices
-template <int WF, int XF, bool XS, int OUT, bool RAWB = false>
+// (BIG_G = false: the caller never passes more than 64 groups, and the
+// 11-group, 8-slice variant is not instantiated)
+template <int WF, int XF, bool XS, int OUT, bool RAWB = false, bool BIG_G = true>
 clove_status_t stream_by_k(const Args& a, hipStream_t stream) {
     const int G = a.G;
     if (G <= 16) return launch_stream<WF, XF, 8, 2, XS, OUT, RAWB>(a, stream);
     if (G <= 22) return launch_stream<WF, XF, 11, 2, XS, OUT, RAWB>(a, stream);
     if (G <= 32) return launch_stream<WF, XF, 8, 4, XS, OUT, RAWB>(a, stream);
     if (G <= 44) return launch_stream<WF, XF, 11, 4, XS, OUT, RAWB>(a, stream);
-    if (G <= 64) return launch_stream<WF, XF, 8, 8, XS, OUT, RAWB>(a, stream);
-    return launch_stream<WF, XF, 11, 8, XS, OUT, RAWB>(a, stream);
+    if (!BIG_G || G <= 64) return launch_stream<WF, XF, 8, 8, XS, OUT, RAWB>(a, stream);
+    if constexpr (BIG_G) return launch_stream<WF, XF, 11, 8, XS, OUT, RAWB>(a, stream);
+    return CLOVE_ERR_INVALID_ARG;
 }
 
 constexpr int kStreamMaxGroups = 88;  // K <= 11264
@@ -125,11 +128,18 @@ constexpr int kStreamMaxGroups = 88;  // K <= 11264
 // Two weight fragments (32 rows) per workgroup when that still gives every
 // CU a workgroup, else one (measured on the 11008 x 4096 and 4096 x 11008
 // shapes: 32 rows and 4 slices, 16 rows and 8 slices)
+// INT4 (XS) reaches this with at most 16 columns, so only one X fragment.
+// Two X fragments with two weight fragments and 11-group slices (K > 8192)
+// need more registers than a lane has: those take one weight fragment.
 template <bool XS, int OUT>
 clove_status_t run_stream(const Args& a, int cus, hipStream_t stream) {
     const bool wf2 = cdiv(a.R, 32) >= cus;
-    if (a.C <= 16) return wf2 ? stream_by_k<2, 1, XS, OUT>(a, stream) : stream_by_k<1, 1, XS, OUT>(a, stream);
-    return wf2 ? stream_by_k<2, 2, XS, OUT>(a, stream) : stream_by_k<1, 2, XS, OUT>(a, stream);
+    if (XS || a.C <= 16) return wf2 ? stream_by_k<2, 1, XS, OUT>(a, stream) : stream_by_k<1, 1, XS, OUT>(a, stream);
+    if constexpr (!XS) {
+        if (wf2 && a.G <= 64) return stream_by_k<2, 2, XS, OUT, false, false>(a, stream);
+        return stream_by_k<1, 2, XS, OUT>(a, stream);
+    }
+    return CLOVE_ERR_INVALID_ARG;
 }
 
 }  // namespace

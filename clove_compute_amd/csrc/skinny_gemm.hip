@@ -12,6 +12,14 @@ using namespace sk;
 using F16M32 = Cfg<false, 32, 128, 1, 4, 5>;
 using F16M64 = Cfg<false, 64, 128, 2, 2, 4>;
 using F16M128 = Cfg<false, 128, 64, 4, 1, 4>;
+// mid-size shapes (M > 256) whose 256x256 tile grid would leave CUs idle:
+// 128x128 tiles (waves of 64x64), or 64x64 tiles when even those are too few
+// (hot launches: 2048^3 25 us with 128x128 against 45 us on the generic
+// register-staged kernel; 1024^3 8 us with 64x64 against 13 us with 128x128
+// and 21 us generic; 512x4096x4096 29 us with 128x128 in two K splits
+// against 33 us with 128x64)
+using F16T128 = Cfg<false, 128, 128, 2, 2, 3>;
+using F16T64 = Cfg<false, 64, 64, 2, 2, 6>;
 using I8M32 = Cfg<true, 32, 128, 1, 4, 5>;
 using I8M64 = Cfg<true, 64, 128, 2, 2, 4>;
 using I8M128 = Cfg<true, 128, 64, 4, 1, 4>;
@@ -35,7 +43,7 @@ clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
     a.nsplit = cdiv(nk, kt_per);
     if (a.nsplit > 1) {
         Scratch s;
-        const size_t bytes = (size_t)tiles * a.nsplit * CF::NT * CF::FM * CF::FN * 16 * sizeof(float);
+        const size_t bytes = (size_t)tiles * a.nsplit * CF::NT * CF::NB * CF::FM * CF::FN * 16 * sizeof(float);
         const clove_status_t st = acquire_scratch(stream, bytes, (size_t)tiles, &s);
         if (st != CLOVE_OK) return st;
         a.part = s.partials;
@@ -52,15 +60,45 @@ clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
 
 bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 
+// The FP16 tile shapes, chosen by shape alone (so that the fused SwiGLU below
+// picks the same tiles, and with them the same split plan, as the two GEMMs
+// it replaces).
+enum class F16Tile { kM32, kM64, kM128, kT128, kT64 };
+
+F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
+    if (M > 256) {
+        const int64_t t128 = (int64_t)cdiv(M, 128) * cdiv(N, 128) * batch;
+        return t128 >= cus / 2 ? F16Tile::kT128 : F16Tile::kT64;
+    }
+    // short K with few 128-row tiles: the 32-row tiles make 4x the workgroups
+    // without a split (512^3: 6.1 us against 7.2, measured)
+    const bool short_k = K <= 16 * F16M128::BK &&
+                         (int64_t)cdiv(M, F16M128::BM) * cdiv(N, F16M128::BN) * batch < cus / 2;
+    if (M <= 32 || (M > 64 && short_k)) return F16Tile::kM32;
+    if (M <= 64) return F16Tile::kM64;
+    return F16Tile::kM128;
+}
+
+bool f16_domain(const void* A, const void* B, const void* C, int M, int N, int K) {
+    if (M <= 4 || K <= 0 || K % 64 != 0 || N < 8 || N % 8 != 0) return false;
+    if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return false;
+    // (the DMA offsets of the padded rows m < M + 128 must stay 32-bit)
+    return fits31((int64_t)(M + 128) * K * 2) && fits31((int64_t)K * N * 2) && fits31((int64_t)M * N * 2);
+}
+
+// two-B-operand (gate, up) counterparts of the tiles above; fewer stages
+// where both B tiles would not fit the LDS
+using SwM32 = Cfg<false, 32, 128, 1, 4, 4, 2>;
+using SwM64 = Cfg<false, 64, 128, 2, 2, 4, 2>;
+using SwM128 = Cfg<false, 128, 64, 4, 1, 4, 2>;
+using SwT128 = Cfg<false, 128, 128, 2, 2, 3, 2>;
+using SwT64 = Cfg<false, 64, 64, 2, 2, 6, 2>;
+
 }  // namespace
 
 bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N, int K,
                      float alpha, float beta, int cus, hipStream_t stream, clove_status_t* status) {
-    if (M <= 4 || M > 512 || K <= 0 || K % 64 != 0 || N < 8 || N % 8 != 0) return false;
-    if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return false;
-    // (the DMA offsets of the padded rows m < M + 128 must stay 32-bit)
-    if (!fits31((int64_t)(M + 128) * K * 2) || !fits31((int64_t)K * N * 2) || !fits31((int64_t)M * N * 2))
-        return false;
+    if (!f16_domain(A, B, C, M, N, K)) return false;
     Args a{};
     a.A = A;
     a.B = B;
@@ -73,13 +111,38 @@ bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batc
     a.sA = (int64_t)M * K;
     a.sB = (int64_t)K * N;
     a.sC = (int64_t)M * N;
-    // short K with few 128-row tiles: the 32-row tiles make 4x the workgroups
-    // without a split (512^3: 6.1 us against 7.2, measured)
-    const bool short_k = K <= 16 * F16M128::BK &&
-                         (int64_t)cdiv(M, F16M128::BM) * cdiv(N, F16M128::BN) * batch < cus / 2;
-    if (M <= 32 || (M > 64 && short_k)) *status = run<F16M32, kF16AlphaBeta>(a, batch, cus, stream);
-    else if (M <= 64) *status = run<F16M64, kF16AlphaBeta>(a, batch, cus, stream);
-    else *status = run<F16M128, kF16AlphaBeta>(a, batch, cus, stream);
+    switch (pick_f16_tile(batch, M, N, K, cus)) {
+        case F16Tile::kM32: *status = run<F16M32, kF16AlphaBeta>(a, batch, cus, stream); break;
+        case F16Tile::kM64: *status = run<F16M64, kF16AlphaBeta>(a, batch, cus, stream); break;
+        case F16Tile::kM128: *status = run<F16M128, kF16AlphaBeta>(a, batch, cus, stream); break;
+        case F16Tile::kT128: *status = run<F16T128, kF16AlphaBeta>(a, batch, cus, stream); break;
+        case F16Tile::kT64: *status = run<F16T64, kF16AlphaBeta>(a, batch, cus, stream); break;
+    }
+    return true;
+}
+
+bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
+                       int hidden, int inter, int cus, hipStream_t stream, clove_status_t* status) {
+    if (!f16_domain(X, W_gate, out, T, inter, hidden) || !aligned16(W_up)) return false;
+    Args a{};
+    a.A = X;
+    a.B = W_gate;
+    a.B2 = W_up;
+    a.C = out;
+    a.alpha = 1.0f;
+    a.M = T;
+    a.N = inter;
+    a.K = hidden;
+    a.sA = (int64_t)T * hidden;
+    a.sB = (int64_t)hidden * inter;
+    a.sC = (int64_t)T * inter;
+    switch (pick_f16_tile(1, T, inter, hidden, cus)) {
+        case F16Tile::kM32: *status = run<SwM32, kF16SwiGLU>(a, 1, cus, stream); break;
+        case F16Tile::kM64: *status = run<SwM64, kF16SwiGLU>(a, 1, cus, stream); break;
+        case F16Tile::kM128: *status = run<SwM128, kF16SwiGLU>(a, 1, cus, stream); break;
+        case F16Tile::kT128: *status = run<SwT128, kF16SwiGLU>(a, 1, cus, stream); break;
+        case F16Tile::kT64: *status = run<SwT64, kF16SwiGLU>(a, 1, cus, stream); break;
+    }
     return true;
 }
 

@@ -25,6 +25,14 @@
 // Split-K over workgroups (whole K tiles) when the tile grid does not cover
 // the CUs, with the shared publish / reduce (split order, deterministic;
 // int32 partials for INT8, so the integer accumulator stays exact).
+//
+// Two B operands (NB = 2, FP16 only): B and B2 share A and the tile's
+// columns; each stage holds A, then the B tile, then the B2 tile, and every
+// wave keeps both accumulator sets.  The SwiGLU epilogue (kF16SwiGLU) then
+// writes fp16(silu(fp16(A@B)) * fp16(A@B2)) -- gate and up of an MLP -- with
+// neither projection reaching memory.  Each accumulator sums its k in the
+// same order as the one-operand kernel with the same BM, BN and split plan,
+// so gate and up are bit-identical to two separate GEMMs.
 #pragma once
 
 #include "common.hpp"
@@ -38,11 +46,12 @@ using dma::dma16;
 using dma::make_rsrc;
 using dma::vmcnt_imm;
 
-enum Out { kF16AlphaBeta = 0, kI8Tensor = 1, kI8RowCol = 2, kI8Acc32 = 3 };
+enum Out { kF16AlphaBeta = 0, kI8Tensor = 1, kI8RowCol = 2, kI8Acc32 = 3, kF16SwiGLU = 4 };
 
 struct Args {
     const void* A;       // [batch][M, K]
     const void* B;       // [batch][K, N]
+    const void* B2;      // [batch][K, N], second B operand (NB = 2)
     void* C;             // [batch][M, N]  fp16, or int32 for kI8Acc32
     const uint16_t* sa;  // [M] fp16 (kI8RowCol)
     const uint16_t* sb;  // [N] fp16 (kI8RowCol)
@@ -55,20 +64,21 @@ struct Args {
     unsigned* counters;
 };
 
-template <bool I8_, int BM_, int BN_, int WM_, int WN_, int S_>
+template <bool I8_, int BM_, int BN_, int WM_, int WN_, int S_, int NB_ = 1>
 struct Cfg {
     static constexpr bool I8 = I8_;
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, S = S_;
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, S = S_, NB = NB_;
     static constexpr int ES = I8 ? 1 : 2;  // bytes per element
     static constexpr int NW = WM * WN, NT = 64 * NW;
     static constexpr int BK = 128 / ES;    // K per stage: 128 bytes of every A row
     static constexpr int BNB = BN * ES;    // bytes of one B k-row in the tile
     static constexpr int FM = BM / (32 * WM), FN = BN / (32 * WN);
     static constexpr int A_BYTES = BM * 128, B_BYTES = BK * BNB;
-    static constexpr int SB = A_BYTES + B_BYTES;
-    static constexpr int DA = A_BYTES / 1024 / NW, DB = B_BYTES / 1024 / NW;
-    static constexpr int D = DA + DB;  // DMA instructions per thread per stage
+    static constexpr int SB = A_BYTES + NB * B_BYTES;
+    static constexpr int DA = A_BYTES / 1024 / NW, DB = B_BYTES / 1024 / NW;  // DB per B operand
+    static constexpr int D = DA + NB * DB;  // DMA instructions per thread per stage
     static_assert(NW == 4, "four waves");
+    static_assert(NB == 1 || (NB == 2 && !I8), "two B operands: FP16 only");
     static_assert(FM >= 1 && FN >= 1 && BM == 32 * FM * WM && BN == 32 * FN * WN, "wave tiles");
     static_assert(BNB == 64 || BNB == 128 || BNB == 256 || BNB == 512, "B row bytes");
     static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
@@ -157,6 +167,9 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
     const unsigned char* Bb = static_cast<const unsigned char*>(p.B) + batch * p.sB * ES;
     const u32x4 ra = make_rsrc(Ab, (unsigned)M * K * ES);
     const u32x4 rb = make_rsrc(Bb, (unsigned)K * N * ES);
+    const u32x4 rb2 = CF::NB == 2
+        ? make_rsrc(static_cast<const unsigned char*>(p.B2) + batch * p.sB * ES, (unsigned)K * N * ES)
+        : rb;
 
     // ---- per-lane DMA offsets (fixed over K; the K position is the soffset) ----
     int offa[CF::DA], offb[CF::DB];
@@ -179,6 +192,11 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 #pragma unroll
         for (int i = 0; i < CF::DB; ++i)
             dma16(rb, st + CF::A_BYTES + (wave * CF::DB + i) * 1024, offb[i], k0 * N * ES);
+        if constexpr (CF::NB == 2) {
+#pragma unroll
+            for (int i = 0; i < CF::DB; ++i)
+                dma16(rb2, st + CF::A_BYTES + CF::B_BYTES + (wave * CF::DB + i) * 1024, offb[i], k0 * N * ES);
+        }
     };
 
     // ---- fragment addressing (relative to the stage) ----
@@ -208,13 +226,17 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 
     typedef typename std::conditional<I8, i32x16, f32x16>::type AccT;
     typedef typename std::conditional<I8, i32x4, f32x4>::type AccT4;
-    AccT acc[FN][FM];
+    constexpr int NB = CF::NB;
+    static_assert((OUT == kF16SwiGLU) == (NB == 2), "the SwiGLU epilogue takes two B operands");
+    AccT acc[NB][FN][FM];
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+            for (int j = 0; j < FM; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[b][i][j][v] = 0;
 
 #pragma unroll
     for (int t = 0; t < S - 1; ++t)
@@ -230,57 +252,66 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            u32x4 af[FM], bf[FN];
+            u32x4 af[FM];
             const unsigned ab = st + aoff[ks];
 #pragma unroll
             for (int j = 0; j < FM; ++j) af[j] = lds_read16(ab + 4096 * j);
 #pragma unroll
-            for (int i = 0; i < FN; ++i) {
-                const u32x2 lo = lds_read_tr<I8>(st + boff[ks][0][i]);
-                const u32x2 hi = lds_read_tr<I8>(st + boff[ks][1][i]);
-                bf[i] = u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
+            for (int b = 0; b < NB; ++b) {
+                u32x4 bf[FN];
 #pragma unroll
-            for (int i = 0; i < FN; ++i)
-#pragma unroll
-                for (int j = 0; j < FM; ++j) {
-                    if constexpr (I8)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bitcast<i32x4>(bf[i]),
-                                                                          bitcast<i32x4>(af[j]), acc[i][j], 0, 0, 0);
-                    else
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bitcast<f16x8>(bf[i]),
-                                                                           bitcast<f16x8>(af[j]), acc[i][j], 0, 0, 0);
+                for (int i = 0; i < FN; ++i) {
+                    const u32x2 lo = lds_read_tr<I8>(st + b * CF::B_BYTES + boff[ks][0][i]);
+                    const u32x2 hi = lds_read_tr<I8>(st + b * CF::B_BYTES + boff[ks][1][i]);
+                    bf[i] = u32x4{lo.x, lo.y, hi.x, hi.y};
                 }
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < FM; ++j) {
+                        if constexpr (I8)
+                            acc[b][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                                bitcast<i32x4>(bf[i]), bitcast<i32x4>(af[j]), acc[b][i][j], 0, 0, 0);
+                        else
+                            acc[b][i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                bitcast<f16x8>(bf[i]), bitcast<f16x8>(af[j]), acc[b][i][j], 0, 0, 0);
+                    }
+            }
         }
     }
 
     // ---- split-K ----
     if (p.nsplit > 1) {
-        constexpr int NC = FN * FM * 4;
+        constexpr int NC = NB * FN * FM * 4;
         f32x4 v[NC];
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int j = 0; j < FM; ++j)
+            for (int i = 0; i < FN; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    v[(i * FM + j) * 4 + q] = bitcast<f32x4>(
-                        AccT4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+                for (int j = 0; j < FM; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        v[((b * FN + i) * FM + j) * 4 + q] = bitcast<f32x4>(
+                            AccT4{acc[b][i][j][4 * q], acc[b][i][j][4 * q + 1], acc[b][i][j][4 * q + 2],
+                                  acc[b][i][j][4 * q + 3]});
         float* slabs = p.part + (size_t)tile * p.nsplit * NC * CF::NT * 4;
         splitk_publish<NC, CF::NT>(slabs + (size_t)split * NC * CF::NT * 4, tid, v);
         if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
             return;
         splitk_reduce<NC, CF::NT, I8>(slabs, p.nsplit, tid, v);
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int j = 0; j < FM; ++j)
+            for (int i = 0; i < FN; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const AccT4 w = bitcast<AccT4>(v[(i * FM + j) * 4 + q]);
+                for (int j = 0; j < FM; ++j)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = w[e];
-                }
+                    for (int q = 0; q < 4; ++q) {
+                        const AccT4 w = bitcast<AccT4>(v[((b * FN + i) * FM + j) * 4 + q]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[b][i][j][4 * q + e] = w[e];
+                    }
     }
 
     // ---- epilogue: lane row m, runs of 4 columns ----
@@ -334,13 +365,13 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
                 if constexpr (OUT == kI8Acc32) {
                     int* dst = reinterpret_cast<int*>(Cb) + (int64_t)m * N + n;
                     *reinterpret_cast<i32x4*>(dst) =
-                        i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                        i32x4{acc[0][i][j][4 * q], acc[0][i][j][4 * q + 1], acc[0][i][j][4 * q + 2], acc[0][i][j][4 * q + 3]};
                 } else {
                     uint16_t* dst = reinterpret_cast<uint16_t*>(Cb) + (int64_t)m * N + n;
                     float r[4];
                     if constexpr (OUT == kF16AlphaBeta) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) r[e] = p.alpha * acc[i][j][4 * q + e];
+                        for (int e = 0; e < 4; ++e) r[e] = p.alpha * acc[0][i][j][4 * q + e];
                         if (p.beta != 0.0f) {
                             const u32x2 c = oldc[j][i][q];
                             r[0] = fmaf(p.beta, h2f(c.x & 0xffffu), r[0]);
@@ -348,12 +379,21 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
                             r[2] = fmaf(p.beta, h2f(c.y & 0xffffu), r[2]);
                             r[3] = fmaf(p.beta, h2f(c.y >> 16), r[3]);
                         }
+                    } else if constexpr (OUT == kF16SwiGLU) {
+                        // gate and up rounded to fp16 as two GEMM outputs would be
+                        const uint16_t o0 = swiglu_h(f2h(acc[0][i][j][4 * q]), f2h(acc[NB - 1][i][j][4 * q]));
+                        const uint16_t o1 = swiglu_h(f2h(acc[0][i][j][4 * q + 1]), f2h(acc[NB - 1][i][j][4 * q + 1]));
+                        const uint16_t o2 = swiglu_h(f2h(acc[0][i][j][4 * q + 2]), f2h(acc[NB - 1][i][j][4 * q + 2]));
+                        const uint16_t o3 = swiglu_h(f2h(acc[0][i][j][4 * q + 3]), f2h(acc[NB - 1][i][j][4 * q + 3]));
+                        *reinterpret_cast<u32x2*>(dst) = u32x2{(unsigned)o0 | ((unsigned)o1 << 16),
+                                                               (unsigned)o2 | ((unsigned)o3 << 16)};
+                        continue;
                     } else if constexpr (OUT == kI8Tensor) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[i][j][4 * q + e]) * p.scale;
+                        for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[0][i][j][4 * q + e]) * p.scale;
                     } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[i][j][4 * q + e]) * (sa * sbv[i][q][e]);
+                        for (int e = 0; e < 4; ++e) r[e] = static_cast<float>(acc[0][i][j][4 * q + e]) * (sa * sbv[i][q][e]);
                     }
                     *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r[0], r[1]), pack2h(r[2], r[3])};
                 }

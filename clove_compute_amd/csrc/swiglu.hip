@@ -7,9 +7,15 @@
 //    (8 elements per thread), grid-stride; a scalar tail for n % 8 and for
 //    unaligned pointers.
 //  * swiglu_fused on FP16 weights [hidden, intermediate] (the reference's
-//    gemm_fp16 B layout): gate into the output, up into a library buffer,
-//    both through gemm_fp16, then SwiGLU in place.  (The INT4-weight MLP path,
-//    launch_w4a16_swiglu, fuses the pair inside the GEMM instead.)
+//    gemm_fp16 B layout), one launch that writes neither projection to
+//    memory: the FP16 GEMV with two weight operands for T <= 4, the skinny
+//    MFMA kernel with two B operands for T > 4 (both bit-identical to two
+//    gemm_fp16 calls followed by swiglu on the shapes where gemm_fp16 takes
+//    the same kernel family), and for shapes outside both (unaligned
+//    operands, hidden % 64 != 0 at T > 4) swiglu_fused_direct: one thread per
+//    output column and up to four tokens, fp32 fmaf over k in order -- the
+//    arithmetic of the reference's naive kernel (src/kernels/gemm_fp16.cu:
+//    241-262) for both projections.
 #include <algorithm>
 
 #include "common.hpp"
@@ -45,6 +51,38 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t* gate,
     for (; i < n; i += stride) out[i] = swiglu_h(gate[i], up[i]);
 }
 
+// out[t, i] = swiglu(fp16(sum_k X[t,k] Wg[k,i]), fp16(sum_k X[t,k] Wu[k,i])),
+// sums in fp32 with fmaf in k order; thread = column i, tokens t0..t0+TT-1.
+// Weight reads are coalesced along i; X reads are the same address across
+// the wave (one broadcast per k).
+template <int TT>
+__global__ void __launch_bounds__(256) swiglu_fused_direct(const uint16_t* X, const uint16_t* Wg,
+                                                           const uint16_t* Wu, uint16_t* out, int T,
+                                                           int H, int I) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int t0 = blockIdx.y * TT;
+    if (i >= I) return;
+    float g[TT], u[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) g[t] = u[t] = 0.0f;
+    const uint16_t* xr[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) xr[t] = X + (int64_t)min(t0 + t, T - 1) * H;
+    for (int k = 0; k < H; ++k) {
+        const float wg = h2f(Wg[(int64_t)k * I + i]);
+        const float wu = h2f(Wu[(int64_t)k * I + i]);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const float x = h2f(xr[t][k]);
+            g[t] = fmaf(x, wg, g[t]);
+            u[t] = fmaf(x, wu, u[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+        if (t0 + t < T) out[(int64_t)(t0 + t) * I + i] = swiglu_h(f2h(g[t]), f2h(u[t]));
+}
+
 }  // namespace act
 
 clove_status_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n,
@@ -64,13 +102,17 @@ clove_status_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t*
 
 clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up,
                                         uint16_t* out, int T, int hidden, int inter, hipStream_t stream) {
-    void* ubuf = nullptr;
-    clove_status_t st = acquire_buffer(stream, kBufSwiglu, (size_t)T * inter * 2, &ubuf);
+    DeviceInfo dev;
+    clove_status_t st = current_device_info(&dev);
     if (st != CLOVE_OK) return st;
-    uint16_t* u = static_cast<uint16_t*>(ubuf);
-    if ((st = launch_gemm_fp16(X, W_gate, out, 1, T, inter, hidden, 1.0f, 0.0f, stream)) != CLOVE_OK) return st;
-    if ((st = launch_gemm_fp16(X, W_up, u, 1, T, inter, hidden, 1.0f, 0.0f, stream)) != CLOVE_OK) return st;
-    return launch_swiglu(out, u, out, (int64_t)T * inter, stream);
+    if (try_gemv_swiglu(X, W_gate, W_up, out, T, hidden, inter, stream, &st)) return st;
+    if (try_skinny_swiglu(X, W_gate, W_up, out, T, hidden, inter, dev.num_cus, stream, &st)) return st;
+    constexpr int TT = 4;
+    const dim3 grid((unsigned)hw::cdiv(inter, 256), (unsigned)hw::cdiv(T, TT));
+    if (grid.y > 65535u) return CLOVE_ERR_INVALID_DIM;
+    CLOVE_LAUNCH(act::swiglu_fused_direct<TT>, grid, dim3(256), 0, stream, X, W_gate, W_up, out, T, hidden,
+                 inter);
+    return check_launch();
 }
 
 }  // namespace clove

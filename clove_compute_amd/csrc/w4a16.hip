@@ -60,8 +60,16 @@ __host__ __device__ constexpr int xperm(int k) { return (k & ~7) | ((k & 1) << 2
 // and the output is H [T, O] = swiglu(fp16(gate), fp16(up)); a wave takes RPW/2
 // gate rows and the RPW/2 up rows of the same outputs, so the pair meets in
 // one lane's registers.
+// Threads per workgroup: as for the other GEMVs, except that four rows of two
+// chunks each (and their scales / zero points) need more than the 128 VGPRs a
+// 1024-thread workgroup leaves
+template <int TV, int RPW, int UPR, bool ALIGNED>
+__host__ __device__ constexpr int w4_max_threads() {
+    return (RPW >= 4 && UPR >= 2) ? 512 : gemv_max_threads<TV, ALIGNED, 2>();
+}
+
 template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false>
-__global__ void __launch_bounds__((gemv_max_threads<TV, ALIGNED, 2>())) w4a16_gemv(GemvParams p) {
+__global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a16_gemv(GemvParams p) {
     static_assert(!SWIGLU || RPW % 2 == 0, "gate / up row pairs");
     constexpr int LR = SWIGLU ? RPW / 2 : RPW;  // output rows per wave
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
@@ -272,7 +280,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
 template <int TV, int RPW, int UPR, bool SWIGLU = false>
 clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(TV, p.nch);
-    wpb = min(wpb, (aligned ? gemv_max_threads<TV, true, 2>() : gemv_max_threads<TV, false, 2>()) / 64);
+    wpb = min(wpb, (aligned ? w4_max_threads<TV, RPW, UPR, true>() : w4_max_threads<TV, RPW, UPR, false>()) / 64);
     const dim3 grid(cdiv(p.O, wpb * (SWIGLU ? RPW / 2 : RPW)));
     auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true, SWIGLU> : w4a16_gemv<TV, RPW, UPR, false, SWIGLU>;
     if (lds > 64 * 1024 &&
@@ -288,7 +296,12 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
 template <int TV>
 clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
     const GemvShape g = gemv_shape(2 * p.O, p.nch, cus);
-    if (g.rpw <= 2) return run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
+    // (a lane loads no more chunks per row than the row has: two-row waves
+    // take 1, 2 or 4 chunk loads per row)
+    if (g.rpw == 1) return run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1, true>(p, g.wpb, aligned, stream)
+                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2, true>(p, g.wpb, aligned, stream)
+                                        : run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
     if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1, true>(p, g.wpb, aligned, stream)
                                       : run_gemv_shape<TV, 4, 2, true>(p, g.wpb, aligned, stream);
     return run_gemv_shape<TV, 8, 1, true>(p, g.wpb, aligned, stream);
@@ -305,8 +318,9 @@ clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t 
         if (g.upr >= 2) return run_gemv_shape<TV, 1, 2>(p, g.wpb, aligned, stream);
         return run_gemv_shape<TV, 1, 1>(p, g.wpb, aligned, stream);
     }
-    if (g.rpw == 2) return g.upr == 1 ? run_gemv_shape<TV, 2, 1>(p, g.wpb, aligned, stream)
-                                      : run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1>(p, g.wpb, aligned, stream)
+                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2>(p, g.wpb, aligned, stream)
+                                        : run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
     if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1>(p, g.wpb, aligned, stream)
                                       : run_gemv_shape<TV, 4, 2>(p, g.wpb, aligned, stream);
     return run_gemv_shape<TV, 8, 1>(p, g.wpb, aligned, stream);

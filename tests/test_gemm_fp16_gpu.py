@@ -254,3 +254,41 @@ def test_skinny_small_integers_bit_exact(M, N, K):
     C = run_fp16(A, B)
     ref = oracle.gemm_fp16_f64(A, B).astype(np.float16)
     assert np.array_equal(f16bits(C), f16bits(ref))
+
+
+# M = 2..4 on the GEMV with several K splits (K > 256): the per-row partials,
+# split publication and reduce of every row count, beta != 0; small integers
+# make every order exact, so the comparison is bit for bit
+@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 1024, 2048), (4, 1024, 2048)])
+def test_gemv_multirow_split_k_bit_exact(M, N, K):
+    g = rng("gemv-mm", M, N, K)
+    A = g.integers(-3, 4, (M, K)).astype(np.float16)
+    B = g.integers(-3, 4, (K, N)).astype(np.float16)
+    C0 = g.integers(-8, 9, (M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=1.0, beta=0.5)
+    exact = A.astype(np.float64) @ B.astype(np.float64) + 0.5 * C0.astype(np.float64)
+    assert np.array_equal(f16bits(C), f16bits(exact.astype(np.float16)))
+
+
+# M > 256 whose 256x256 tile grid would leave CUs idle: 128x128 tiles (with
+# two K splits at 512x4096x4096) or 64x64 tiles (1024^3, and ragged edges)
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (1024, 1024, 1024), (2048, 2048, 2048),
+                                   (300, 1000, 640), (777, 520, 192)])
+def test_mid_size_tiles(M, N, K):
+    g = rng("mid", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.05).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=0.5, beta=0.25)
+    rows = np.unique(np.concatenate([[0, 63, 64, 127, 128, M - 1], g.integers(0, M, 24)]))
+    check_rows(A, B, C, rows, C0, 0.5, 0.25)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (1024, 1024, 1024), (600, 392, 320)])
+def test_mid_size_tiles_small_integers_bit_exact(M, N, K):
+    g = rng("mid-int", M, N, K)
+    A = g.integers(-2, 3, (M, K)).astype(np.float16)
+    B = g.integers(-2, 3, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(f16bits(C), f16bits(exact.astype(np.float16)))

@@ -123,3 +123,25 @@ def test_skinny_bit_exact(M, N, K):
     assert np.array_equal(run_acc32(A, B), accref)
     assert np.array_equal(f16bits(to_host(C1)), f16bits(Cref1))
     assert np.array_equal(f16bits(to_host(C2)), f16bits(Cref2))
+
+
+# M = 2..4 on the GEMV with several K splits, non-zero zero points: per-tensor,
+# row/column scales and the raw accumulators, each bit for bit
+@pytest.mark.parametrize("M,N,K,za,zb", [(2, 4096, 4096, 3, -5), (3, 512, 2048, -7, 11), (4, 512, 2048, 9, -2),
+                                         (4, 4096, 4096, 0, 0)])
+def test_gemv_multirow_split_k(M, N, K, za, zb):
+    g = rng("gemv8-mm", M, N, K, za, zb)
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    sa = g.uniform(0.001, 0.02, M).astype(np.float16)
+    sb = g.uniform(0.001, 0.02, N).astype(np.float16)
+    s1, s2 = np.float32(g.uniform(0.001, 0.05)), np.float32(g.uniform(0.001, 0.05))
+    C1, C2 = empty_f16(M, N), empty_f16(M, N)
+    _cg().gemm_int8(to_dev(A), to_dev(B), C1, M, N, K, float(s1), za, float(s2), zb)
+    _cg().gemm_int8_rowcol(to_dev(A), to_dev(B), to_dev(sa), to_dev(sb), C2, M, N, K, za, zb)
+    _sync()
+    Cref1, accref = oracle.gemm_int8(A, B, s1, za, s2, zb)
+    Cref2, _ = oracle.gemm_int8_rowcol(A, B, sa, sb, za, zb)
+    assert np.array_equal(run_acc32(A, B, za, zb), accref)
+    assert np.array_equal(f16bits(to_host(C1)), f16bits(Cref1))
+    assert np.array_equal(f16bits(to_host(C2)), f16bits(Cref2))

@@ -7,7 +7,9 @@
   met inside a workgroup) for larger T, the two W4A16 layers and the
   elementwise pass for K % 128 != 0 or unaligned operands
 * clove_swiglu_fused -- the reference's declared swiglu_fused
-  (include/clove/kernels/activations.cuh:37-46) on FP16 weights
+  (include/clove/kernels/activations.cuh:37-46) on FP16 weights, one launch
+  with no intermediate buffer, bit-identical to two gemm_fp16 calls and
+  swiglu on the shapes where those take the same kernel family
 
 The checker is the oracle: swiglu restated in C (fp32 silu with libm expf),
 W4A16 in float64.  Device expf and libm expf may differ by an fp32 ulp, which
@@ -182,19 +184,86 @@ def test_w4a16_swiglu_equals_layers_then_swiglu():
 
 
 # ---- FP16 swiglu_fused (the reference's declaration) ----
+# One launch, no intermediate: the FP16 GEMV with two weight operands for
+# T <= 4, the skinny MFMA kernel with two B operands for T > 4 (every tile
+# shape: 32x128, 64x128, 128x64, 64x64, 128x128 with and without K splits),
+# and the direct fallback for unaligned operands or hidden % 64 != 0.
 
-@pytest.mark.parametrize("T,H,I", [(1, 2048, 8192), (7, 64, 96), (128, 512, 1000), (512, 1024, 2048)])
-def test_swiglu_fused_fp16(T, H, I):
-    g = rng("swiglu_fused", T, H, I)
-    X = g.standard_normal((T, H)).astype(np.float16)
-    Wg = (g.standard_normal((H, I)) * 0.05).astype(np.float16)
-    Wu = (g.standard_normal((H, I)) * 0.05).astype(np.float16)
+def run_swiglu_fused(X, Wg, Wu, offset=False):
+    T, H = X.shape
+    I = Wg.shape[1]
+    if offset:
+        # 2-byte aligned views one element into larger buffers
+        bx = to_dev(np.concatenate([np.zeros(1, np.float16), X.reshape(-1)]))
+        bg = to_dev(np.concatenate([np.zeros(1, np.float16), Wg.reshape(-1)]))
+        bu = to_dev(np.concatenate([np.zeros(1, np.float16), Wu.reshape(-1)]))
+        bo = empty_f16(T * I + 1, fill=float("nan"))
+        _cg().swiglu_fused(bx.data_ptr() + 2, bg.data_ptr() + 2, bu.data_ptr() + 2, bo.data_ptr() + 2, T, H, I)
+        _sync()
+        return to_host(bo)[1:].reshape(T, I)
     out = empty_f16(T, I, fill=float("nan"))
     _cg().swiglu_fused(to_dev(X), to_dev(Wg), to_dev(Wu), out, T, H, I)
     _sync()
-    got = to_host(out)
+    return to_host(out)
+
+
+def make_mlp(T, H, I, key):
+    g = rng("swiglu_fused", key, T, H, I)
+    X = g.standard_normal((T, H)).astype(np.float16)
+    Wg = (g.standard_normal((H, I)) * 0.05).astype(np.float16)
+    Wu = (g.standard_normal((H, I)) * 0.05).astype(np.float16)
+    return X, Wg, Wu, g
+
+
+@pytest.mark.parametrize("T,H,I", [(1, 2048, 8192), (3, 512, 1000), (7, 64, 96), (40, 1024, 520),
+                                   (64, 512, 1000), (128, 512, 1000), (300, 512, 768),
+                                   (512, 2048, 8192), (1024, 512, 4096)])
+def test_swiglu_fused_fp16(T, H, I):
+    X, Wg, Wu, g = make_mlp(T, H, I, "tol")
+    got = run_swiglu_fused(X, Wg, Wu)
     rows = np.unique(np.concatenate([[0, T - 1], g.integers(0, T, min(T, 8))]))
     gate = oracle.gemm_fp16_f64(X[rows], Wg).astype(np.float32).astype(np.float16)
     up = oracle.gemm_fp16_f64(X[rows], Wu).astype(np.float32).astype(np.float16)
     ok, rep = within_tol(got[rows], oracle.swiglu(gate, up).astype(np.float64))
     assert ok, rep
+
+
+@pytest.mark.parametrize("T,H,I", [(1, 2048, 8192), (2, 1024, 512), (4, 4096, 264), (7, 64, 96),
+                                   (40, 1024, 520), (64, 512, 1000), (128, 4096, 1024), (300, 512, 768),
+                                   (512, 2048, 8192)])
+def test_swiglu_fused_equals_gemms_then_swiglu(T, H, I):
+    # the fused kernels sum gate and up in the order gemm_fp16 does for the
+    # same shape (same tiles, same split plan), so the result is the two
+    # GEMMs followed by swiglu, bit for bit
+    X, Wg, Wu, _ = make_mlp(T, H, I, "bits")
+    got = run_swiglu_fused(X, Wg, Wu)
+    cg = _cg()
+    dX = to_dev(X)
+    gate, up, ref = empty_f16(T, I), empty_f16(T, I), empty_f16(T, I)
+    cg.gemm_fp16(dX, to_dev(Wg), gate, T, I, H)
+    cg.gemm_fp16(dX, to_dev(Wu), up, T, I, H)
+    cg.swiglu(gate, up, ref, T * I)
+    _sync()
+    assert np.array_equal(f16bits(got), f16bits(to_host(ref)))
+
+
+@pytest.mark.parametrize("T,H,I,offset", [(5, 60, 100, False), (3, 100, 30, False), (33, 200, 72, False),
+                                          (2, 256, 128, True), (20, 128, 64, True)])
+def test_swiglu_fused_direct_fallback(T, H, I, offset):
+    # outside the fast kernels' domain: fp32 fmaf over k in order for both
+    # projections, which is the oracle's naive-kernel arithmetic bit for bit;
+    # only expf's last fp32 bit is left free
+    X, Wg, Wu, _ = make_mlp(T, H, I, "direct")
+    got = run_swiglu_fused(X, Wg, Wu, offset=offset)
+    gate = oracle.gemm_fp16(X, Wg)
+    up = oracle.gemm_fp16(X, Wu)
+    assert_swiglu_close(got, oracle.swiglu(gate, up))
+
+
+def test_swiglu_fused_hidden_zero():
+    out = empty_f16(3, 16, fill=float("nan"))
+    dummy = to_dev(np.zeros(64, np.float16))
+    _cg().swiglu_fused(dummy, dummy, dummy, out, 3, 0, 16)
+    _sync()
+    got = to_host(out)
+    assert np.all(got == 0) and not np.any(np.signbit(got))
