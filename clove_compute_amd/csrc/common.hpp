@@ -185,11 +185,11 @@ __device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, in
             f32x4 buf[SB][CG];
 #pragma unroll
             for (int b = 0; b < SB; ++b) {
-                const int sp = min(s0 + b, nsplit - 1);  // past the end: a harmless repeat
+                if (s0 + b >= nsplit) break;  // uniform: no loads past the last split
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
                     buf[b][c] = bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(
-                        r, ((sp * NC + c0 + c) * NT + tid) * 16, 0, kCpolSc1));
+                        r, (((s0 + b) * NC + c0 + c) * NT + tid) * 16, 0, kCpolSc1));
             }
 #pragma unroll
             for (int b = 0; b < SB; ++b) {

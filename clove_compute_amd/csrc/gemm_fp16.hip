@@ -87,12 +87,16 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
 #pragma unroll
         for (int j = 0; j < GV_RPT; ++j)
             xa[m][j] = A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + GV_KL * j, K - 1)];
+    // (kept ahead of the B loads: one A load scheduled after them would make
+    // the first FMA wait for every B row, loads completing in order)
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 bv[GV_RPT];
 #pragma unroll
     for (int j = 0; j < GV_RPT; ++j) {
         const int k = min(kbeg + kl + GV_KL * j, K - 1);
         bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(B + (int64_t)k * N + nc));
     }
+    __builtin_amdgcn_sched_barrier(0);  // every B row requested before the first FMA
 
     float acc[MM][8];
 #pragma unroll
@@ -148,20 +152,17 @@ __global__ void __launch_bounds__(1024) gemv_f16(GemvParams p) {
         if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
         for (int m = 0; m < MM; ++m) sum[m] = 0.0f;
-        // all partials in flight at once, then summed in split order
+        // all partials in flight at once (none past the last split), then
+        // summed in split order
         for (int s0 = 0; s0 < p.nsplit; s0 += 16) {
             float part[16][MM];
 #pragma unroll
             for (int s = 0; s < 16; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
-                    part[s][m] = load_coherent(
-                        &ws_tile[(int64_t)min(s0 + s, p.nsplit - 1) * MM * GV_COLS + m * GV_COLS + col]);
-#pragma unroll
-            for (int s = 0; s < 16; ++s)
-#pragma unroll
-                for (int m = 0; m < MM; ++m)
-                    if (s0 + s >= p.nsplit) part[s][m] = 0.0f;
+                    part[s][m] = s0 + s < p.nsplit
+                                     ? load_coherent(&ws_tile[(int64_t)(s0 + s) * MM * GV_COLS + m * GV_COLS + col])
+                                     : 0.0f;
 #pragma unroll
             for (int s = 0; s < 16; ++s)
 #pragma unroll

@@ -347,12 +347,16 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
 #pragma unroll
         for (int j = 0; j < IV_RPT; ++j)
             xa[m][j] = p.A[(int64_t)min(m, M - 1) * K + min(kbeg + kl + IV_KL * j, K - 1)];
+    // (kept ahead of the B loads: one A load scheduled after them would make
+    // the first product wait for every B row, loads completing in order)
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 bv[IV_RPT];
 #pragma unroll
     for (int j = 0; j < IV_RPT; ++j) {
         const int k = min(kbeg + kl + IV_KL * j, K - 1);
         bv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.B + (int64_t)k * N + nc));
     }
+    __builtin_amdgcn_sched_barrier(0);  // every B row requested before the first product
 
     // Rows of A in passes of at most two (B stays in registers): the 16 column
     // accumulators of four rows would not fit beside the loads in flight.
@@ -413,21 +417,19 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
         if (!splitk_arrive_is_last(&p.counters[cb], (unsigned)p.nsplit, &s_last)) return;
 #pragma unroll
         for (int m = 0; m < MM; ++m) sum[m] = 0;
-        // partials in flight together: 64 registers' worth
-        constexpr int SB = 64 / MM;
+        // up to SB partials in flight together; none loaded past the last
+        // split (the extra coherent loads lengthen the tail measurably)
+        constexpr int SB = MM >= 4 ? 8 : 16;
         for (int s0 = 0; s0 < p.nsplit; s0 += SB) {
             int part[SB][MM];
 #pragma unroll
             for (int s = 0; s < SB; ++s)
 #pragma unroll
                 for (int m = 0; m < MM; ++m)
-                    part[s][m] = __float_as_int(load_coherent(
-                        &ws_tile[(int64_t)min(s0 + s, p.nsplit - 1) * MM * IV_COLS + m * IV_COLS + col]));
-#pragma unroll
-            for (int s = 0; s < SB; ++s)
-#pragma unroll
-                for (int m = 0; m < MM; ++m)
-                    if (s0 + s >= p.nsplit) part[s][m] = 0;
+                    part[s][m] = s0 + s < p.nsplit
+                                     ? __float_as_int(load_coherent(
+                                           &ws_tile[(int64_t)(s0 + s) * MM * IV_COLS + m * IV_COLS + col]))
+                                     : 0;
 #pragma unroll
             for (int s = 0; s < SB; ++s)
 #pragma unroll
