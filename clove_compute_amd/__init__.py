@@ -6,13 +6,14 @@ is its Python host side: the ctypes binding, a mirror of the reference's
 GEMM API over torch device tensors, and the INT4 packing/quantisation helpers.
 """
 from ._lib import (  # noqa: F401
-    CloveError, CLOVE_ERR_WORKSPACE, CLOVE_INT4_GROUPWISE, CLOVE_INT4_REFERENCE_LITERAL,
-    CLOVE_WORKSPACE_MIN_BYTES,
+    CloveError, CLOVE_ERR_SCRATCH_LIMIT, CLOVE_ERR_WORKSPACE, CLOVE_INT4_GROUPWISE,
+    CLOVE_INT4_REFERENCE_LITERAL, CLOVE_NOALLOC_SCRATCH_BYTES, CLOVE_WORKSPACE_MIN_BYTES,
 )
 from .gemm import (  # noqa: F401
     INT4_GROUP_SIZE,
     gemm_fp16,
     gemm_fp16_batched,
+    gemm_fp16_noalloc,
     gemm_int4,
     gemm_int4_ex,
     gemm_int8,

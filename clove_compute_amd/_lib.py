@@ -20,8 +20,10 @@ CLOVE_ERR_OUT_OF_MEMORY = 5
 CLOVE_ERR_LAUNCH = 6
 CLOVE_ERR_NO_DEVICE = 7
 CLOVE_ERR_WORKSPACE = 8
+CLOVE_ERR_SCRATCH_LIMIT = 9
 
 CLOVE_WORKSPACE_MIN_BYTES = 65536
+CLOVE_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 CLOVE_INT4_GROUPWISE = 0
 CLOVE_INT4_REFERENCE_LITERAL = 1
@@ -37,6 +39,7 @@ SIGNATURES = {
     "clove_abi_version": ([], I),
     "clove_gemm_fp16": ([P, P, P, I, I, I, F, F, P], I),
     "clove_gemm_fp16_batched": ([P, P, P, I, I, I, I, F, F, P], I),
+    "clove_gemm_fp16_noalloc": ([P, P, P, I, I, I, F, F, P], I),
     "clove_gemm_int8": ([P, P, P, I, I, I, F, I8, F, I8, P], I),
     "clove_gemm_int8_rowcol": ([P, P, P, P, P, I, I, I, I8, I8, P], I),
     "clove_gemm_int8_acc32": ([P, P, P, I, I, I, I8, I8, P], I),

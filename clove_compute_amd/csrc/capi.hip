@@ -114,6 +114,36 @@ struct CallScope {
     }
 };
 
+// ---------------------------------------------------------------------------
+// clove_gemm_fp16_noalloc: the fixed device array its calls carve their
+// scratch from (counters in its first CLOVE_WORKSPACE_MIN_BYTES, as in a bound
+// workspace).  In host code `scratch` is a host-side stand-in for the symbol,
+// not a device address: the address each device holds its copy at comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocBytes = CLOVE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+std::mutex g_noalloc_mu;
+std::map<int, char*> g_noalloc_ptr;  // device -> address of its `scratch`
+
+clove_status_t noalloc_scratch(hipStream_t stream, char** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    auto it = g_noalloc_ptr.find(dev);
+    if (it == g_noalloc_ptr.end()) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+            return CLOVE_ERR_NO_DEVICE;
+        // the counters start at zero (every call leaves them zero again)
+        hipLaunchKernelGGL(zero_u32, dim3(16), dim3(256), 0, stream, static_cast<unsigned*>(ptr), kWsCounters);
+        if (hipGetLastError() != hipSuccess) return CLOVE_ERR_LAUNCH;
+        it = g_noalloc_ptr.emplace(dev, static_cast<char*>(ptr)).first;
+    }
+    *out = it->second;
+    return CLOVE_OK;
+}
+
 }  // namespace
 
 bool dry_run() { return t_ws.mode == WsMode::kQuery; }
@@ -222,6 +252,9 @@ const char* clove_status_string(clove_status_t status) {
         case CLOVE_ERR_LAUNCH: return "CLOVE_ERR_LAUNCH: kernel launch failed";
         case CLOVE_ERR_NO_DEVICE: return "CLOVE_ERR_NO_DEVICE: no usable HIP device";
         case CLOVE_ERR_WORKSPACE: return "CLOVE_ERR_WORKSPACE: the bound workspace is too small for the call";
+        case CLOVE_ERR_SCRATCH_LIMIT:
+            return "CLOVE_ERR_SCRATCH_LIMIT: the call needs more scratch than the fixed array of "
+                   "clove_gemm_fp16_noalloc holds (CLOVE_NOALLOC_SCRATCH_BYTES)";
     }
     return "CLOVE_ERR_UNKNOWN";
 }
@@ -248,6 +281,31 @@ clove_status_t clove_gemm_fp16_batched(const void* A, const void* B, void* C, in
 clove_status_t clove_gemm_fp16(const void* A, const void* B, void* C, int M, int N, int K,
                                float alpha, float beta, void* stream) {
     return clove_gemm_fp16_batched(A, B, C, 1, M, N, K, alpha, beta, stream);
+}
+
+clove_status_t clove_gemm_fp16_noalloc(const void* A, const void* B, void* C, int M, int N, int K,
+                                       float alpha, float beta, void* stream) {
+    if (t_ws.mode == WsMode::kQuery) {
+        // plan and validate as clove_gemm_fp16; the fixed array is not the
+        // caller's workspace, so the query's size is left as it was
+        const size_t need = t_ws.need;
+        const clove_status_t st = clove_gemm_fp16(A, B, C, M, N, K, alpha, beta, stream);
+        t_ws.need = need;
+        return st;
+    }
+    char* ptr = nullptr;
+    clove_status_t st = noalloc_scratch(static_cast<hipStream_t>(stream), &ptr);
+    if (st != CLOVE_OK) return st;
+    // the call runs with this thread's workspace bound to the array, then the
+    // thread's own mode is restored
+    const ThreadWs saved = t_ws;
+    t_ws = ThreadWs{};
+    t_ws.mode = WsMode::kBound;
+    t_ws.ptr = ptr;
+    t_ws.bytes = kNoAllocBytes;
+    st = clove_gemm_fp16(A, B, C, M, N, K, alpha, beta, stream);
+    t_ws = saved;
+    return st == CLOVE_ERR_WORKSPACE ? CLOVE_ERR_SCRATCH_LIMIT : st;
 }
 
 static clove_status_t int8_common(Int8Args& a, void* stream) {

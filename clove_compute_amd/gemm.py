@@ -45,6 +45,16 @@ def gemm_fp16(A, B, C, M: int, N: int, K: int, alpha: float = 1.0, beta: float =
                                           _stream(stream)), "gemm_fp16")
 
 
+def gemm_fp16_noalloc(A, B, C, M: int, N: int, K: int, alpha: float = 1.0, beta: float = 0.0,
+                      stream=None) -> None:
+    """gemm_fp16 that allocates nothing: split-K scratch from the library's fixed
+    per-GPU array (CLOVE_NOALLOC_SCRATCH_BYTES); raises CloveError with
+    CLOVE_ERR_SCRATCH_LIMIT when the call needs more.  Calls that overlap on one
+    GPU share the array and must be serialised by the caller."""
+    _lib.check(_lib.lib().clove_gemm_fp16_noalloc(_ptr(A), _ptr(B), _ptr(C), M, N, K, alpha, beta,
+                                                  _stream(stream)), "gemm_fp16_noalloc")
+
+
 def gemm_fp16_batched(A, B, C, batch: int, M: int, N: int, K: int, alpha: float = 1.0,
                       beta: float = 0.0, stream=None) -> None:
     _lib.check(_lib.lib().clove_gemm_fp16_batched(_ptr(A), _ptr(B), _ptr(C), batch, M, N, K,

@@ -39,7 +39,9 @@ typedef enum clove_status {
     CLOVE_ERR_OUT_OF_MEMORY = 5,  /* scratch allocation failed */
     CLOVE_ERR_LAUNCH = 6,         /* the HIP runtime rejected a launch */
     CLOVE_ERR_NO_DEVICE = 7,      /* no usable HIP device */
-    CLOVE_ERR_WORKSPACE = 8       /* the bound workspace is too small for the call */
+    CLOVE_ERR_WORKSPACE = 8,      /* the bound workspace is too small for the call */
+    CLOVE_ERR_SCRATCH_LIMIT = 9   /* clove_gemm_fp16_noalloc: the call needs more scratch
+                                     than CLOVE_NOALLOC_SCRATCH_BYTES */
 } clove_status_t;
 
 /* INT4 arithmetic selected by clove_gemm_int4_ex. */
@@ -220,6 +222,27 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
 clove_status_t clove_workspace_bind(void* ptr, size_t bytes);
 clove_status_t clove_workspace_query_begin(void);
 size_t clove_workspace_query_end(void);
+
+/*
+ * clove_gemm_fp16 for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No reference counterpart.  Same arguments, kernels, split plans and results
+ * (bit for bit) as clove_gemm_fp16; it calls no hipMalloc / hipFree and no
+ * allocating library routine.  Its split-K partials and completion counters
+ * live in a fixed device array of CLOVE_NOALLOC_SCRATCH_BYTES per GPU (the
+ * library's static device memory, held until the process ends); a call that
+ * would need more returns CLOVE_ERR_SCRATCH_LIMIT and launches nothing.
+ * Every shape with M <= 512 and N, K <= 8192 whose operands are 16-byte
+ * aligned, with N % 8 == 0 and K % 64 == 0, fits, as do the large shapes
+ * (M, N >= 2048) that split nothing.  The first call on a device clears the array's counters
+ * with one small kernel on `stream`.  Every call on a GPU shares that GPU's
+ * array: calls that may overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.
+ */
+#define CLOVE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+clove_status_t clove_gemm_fp16_noalloc(const void* A, const void* B, void* C,
+                                       int M, int N, int K, float alpha, float beta,
+                                       void* stream);
 
 /* Frees the scratch buffers held for the current device (all streams),
  * including the SwiGLU intermediates and buffers replaced by larger ones.
