@@ -36,10 +36,11 @@ CFLAGS = [
 ]
 
 
-# per-source additions: the INT4-weight GEMM keeps its per-group MFMA sums in
+# per-source additions: the INT4-weight GEMMs keep their per-group MFMA sums in
 # VGPRs (the group fold reads every one of them; in AGPRs each read would be a
 # separate v_accvgpr_read)
-EXTRA = {"i4w_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA = {"i4w_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "i4i4_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _sources():

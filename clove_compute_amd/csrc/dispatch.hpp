@@ -95,6 +95,9 @@ clove_status_t launch_w4a16(const W4A16Args& args, hipStream_t stream);
 // it launches and stores the launch status in *status.
 bool try_i4w_w4a16(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 bool try_i4w_int4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+// group-wise INT4 x INT4 on int8 MFMA (i4i4_gemm.hip): N >= 64, K % 256 == 0,
+// 16-byte aligned A; zero points in [-112, 127] (others give NaN outputs)
+bool try_i4i4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 // SwiGLU of a fused gate/up INT4 weight: args.W holds 2 args.O rows (gate rows,
 // then up rows, scales / zeros likewise), args.Y receives H [T, O]
 bool try_i4w_w4a16_swiglu(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);

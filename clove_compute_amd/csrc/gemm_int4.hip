@@ -461,6 +461,7 @@ clove_status_t launch_gemm_int4(const Int4Args& a, hipStream_t stream) {
     }
     if (!literal) {
         clove_status_t st2;
+        if (try_i4i4(a, dev.num_cus, stream, &st2)) return st2;
         if (try_i4w_int4(a, dev.num_cus, stream, &st2)) return st2;
     }
     mg::Params p{};

@@ -171,3 +171,58 @@ def test_groupwise_stream_path_pow2_bit_exact():
     C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
     _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
     assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))
+
+
+# group-wise with N >= 64 and K % 256 == 0: the int8-MFMA kernel (i4i4_gemm)
+# after the Bt pre-pass.  Zero points at both ends of its exact range
+# [-112, 127] (q - z spans [-127, 127]) with power-of-two scales: every step
+# exact, so bit for bit.
+@pytest.mark.parametrize("M,N,K", [(130, 64, 512), (257, 136, 1024), (1, 64, 256)])
+def test_int8_mfma_path_zero_point_range_bit_exact(M, N, K):
+    g = rng("i4i4-range", M, N, K)
+    G = K // 128
+    A_q = quant.pack_rows(g.integers(0, 16, (M, K)))
+    B_q = quant.pack_cols(g.integers(0, 16, (K, N)))
+    ends = np.array([-112, 127, 0, 15, 8], np.float16)
+    zA = ends[g.integers(0, 5, (M, G))]
+    zB = ends[g.integers(0, 5, (G, N))]
+    # one power of two for every scale: |C| < 2^8 in steps of 2^-16, so the
+    # fp32 sums are exact and the fp16 results finite
+    sA = np.full((M, G), 2.0 ** -8, np.float16)
+    sB = np.full((G, N), 2.0 ** -8, np.float16)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))
+
+
+def test_int8_mfma_path_zero_point_outside_range_is_nan():
+    # a zero point the int8 operands cannot hold exactly poisons exactly the
+    # outputs whose sum it enters (its row, or its column), nothing else
+    M, N, K = 192, 128, 512
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "nan")
+    zA[5, 2] = 200.0
+    zB[1, 77] = -120.0
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    bad = np.zeros((M, N), bool)
+    bad[5, :] = True
+    bad[:, 77] = True
+    assert np.all(np.isnan(C[bad].astype(np.float32)))
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    ok, rep = within_tol(C[~bad], ref[~bad])
+    assert ok, rep
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 128, 11008), (600, 100, 2816), (1000, 320, 1024),
+                                   (11008, 128, 4096), (8192, 512, 512)])
+def test_int8_mfma_path_split_k(M, N, K):
+    # 64-row tiles split over groups (G = 86 in four splits of 22, 22, 22 and
+    # 20 groups; G = 22 in eleven splits of two), N not a multiple of 8
+    # (element stores), two and three column tiles, 64-row tiles without a
+    # split (11008 rows) and 128-row tiles (8192 x 512: 256 tiles)
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "i4i4-split")
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    g = rng("rows-i4i4", M, N, K)
+    rows = np.arange(M) if M <= 1000 else np.unique(np.concatenate([[0, 127, 128, M - 1], g.integers(0, M, 32)]))
+    _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
+    ok, rep = within_tol(C[rows], ref)
+    assert ok, rep
