@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bound on the CPU-baseline sample (0 disables it)")
     ap.add_argument("--skip-extra", action="store_true", help="headline only")
+    ap.add_argument("--floor", action="store_true",
+                    help="only measure the cold HBM streaming-read floor (lib/libclove_diag.so) at the "
+                         "weight sizes of the memory-bound shapes and print one JSON line")
     ap.add_argument("--compare-lib", action="store_true",
                     help="also time torch.matmul (hipBLASLt) on the headline operands, in blocks "
                          "alternating with clove_gemm_fp16, and report both")
@@ -450,6 +453,43 @@ def extras():
     return out
 
 
+def floor():
+    """Cold read floor: a read-only streaming kernel (16-byte lane-contiguous
+    loads, 32 KB per workgroup) over the weight sizes of the decode and
+    memory-bound shapes, each timed as graph replays that rotate through
+    >= 512 MiB of copies (no replay finds its bytes in the 256 MB Infinity
+    Cache), and hot (one copy replayed)."""
+    import ctypes
+
+    import torch
+    path = os.path.join(ROOT, "clove_compute_amd", "lib", "libclove_diag.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    lib.clove_diag_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    lib.clove_diag_stream_read.restype = ctypes.c_int
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, nbytes in (("int8_4096x4096_weight", 4096 * 4096),
+                         ("int4_11008x4096_weight", 11008 * 4096 // 2),
+                         ("fp16_4096x4096_weight", 4096 * 4096 * 2)):
+        bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(copies_for(nbytes))]
+
+        def call(b):
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            if lib.clove_diag_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), stream) <= 0:
+                raise RuntimeError("clove_diag_stream_read failed")
+        calls = [lambda b=b: call(b) for b in bufs]
+        us = graph_time(calls, [], 5)
+        hot = graph_time(calls[:1] * 16, [], 5)
+        out[name] = {"MB": round(nbytes / 1e6, 3), "copies": len(bufs), "us_cold": round(us, 3),
+                     "GBs_cold": round(nbytes / us / 1e3, 1), "us_hot": round(hot, 3),
+                     "GBs_hot": round(nbytes / hot / 1e3, 1)}
+        print(f"[floor] {name}: cold {us:.2f} us, hot {hot:.2f} us", file=sys.stderr, flush=True)
+        del bufs, calls
+    print(json.dumps({"floor": out, "device": device_info()}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -463,6 +503,9 @@ def main():
     torch.cuda.set_device(0)
     from clove_compute_amd import _lib
     _lib.lib()  # fails loudly when the HIP library is not built
+    if args.floor:
+        floor()
+        return
 
     timer = Timer()
     h = headline(args, timer)

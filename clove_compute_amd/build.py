@@ -20,6 +20,9 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libclove_gemm.so")
+# diagnostics for bench.py --floor (not part of the GEMM C-ABI)
+DIAG_SRC = os.path.join(CSRC, "diag")
+DIAG_LIB = os.path.join(LIBDIR, "libclove_diag.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -78,9 +81,18 @@ def build(force: bool = False, jobs: int = 8) -> str:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link of libclove_gemm.so failed")
     os.replace(LIB + ".tmp", LIB)
+    dsrcs = sorted(glob.glob(os.path.join(DIAG_SRC, "*.hip")))
+    dobjs = [_compile(s, force) for s in dsrcs]
+    if dobjs:
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", DIAG_LIB + ".tmp", *dobjs]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise RuntimeError("link of libclove_diag.so failed")
+        os.replace(DIAG_LIB + ".tmp", DIAG_LIB)
     # no kernel that an aligned call can reach may spill registers to scratch
     from clove_compute_amd import resources
-    resources.check(objs)
+    resources.check(objs + dobjs)
     return LIB
 
 
