@@ -18,6 +18,7 @@ from .gemm import (  # noqa: F401
     gemm_int4_ex,
     gemm_int8,
     gemm_int8_acc32,
+    gemm_int4_group_acc32,
     gemm_int8_rowcol,
     gemm_w4a16,
     release_scratch,

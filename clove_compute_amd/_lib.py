@@ -43,6 +43,7 @@ SIGNATURES = {
     "clove_gemm_int8": ([P, P, P, I, I, I, F, I8, F, I8, P], I),
     "clove_gemm_int8_rowcol": ([P, P, P, P, P, I, I, I, I8, I8, P], I),
     "clove_gemm_int8_acc32": ([P, P, P, I, I, I, I8, I8, P], I),
+    "clove_gemm_int4_group_acc32": ([P, P, P, P, P, I, I, I, P], I),
     "clove_gemm_int4": ([P, P, P, P, P, P, P, I, I, I, P], I),
     "clove_gemm_int4_ex": ([P, P, P, P, P, P, P, I, I, I, I, P], I),
     "clove_gemm_w4a16": ([P, P, P, P, P, I, I, I, F, F, P], I),

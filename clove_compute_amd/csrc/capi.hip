@@ -72,6 +72,7 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
 }
 
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 // ---------------------------------------------------------------------------
 // caller-owned workspace (clove_workspace_bind / clove_workspace_query_*), per
@@ -406,6 +407,32 @@ clove_status_t clove_gemm_int4(const uint8_t* A_q, const void* A_scale, const vo
                                void* C, int M, int N, int K, void* stream) {
     return clove_gemm_int4_ex(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M, N, K,
                               CLOVE_INT4_GROUPWISE, stream);
+}
+
+clove_status_t clove_gemm_int4_group_acc32(const uint8_t* A_q, const void* A_zero, const uint8_t* B_q,
+                                           const void* B_zero, int32_t* P, int M, int N, int K,
+                                           void* stream) {
+    CallScope scope;
+    if (M < 0 || N < 0 || K < 0) return CLOVE_ERR_INVALID_DIM;
+    if (M == 0 || N == 0 || K == 0) return CLOVE_OK;
+    if (!A_q || !A_zero || !B_q || !B_zero || !P) return CLOVE_ERR_NULL_POINTER;
+    if (K % 256 != 0 || !aligned16(A_q) || !aligned4(P) || !aligned2(A_zero) || !aligned2(B_zero))
+        return CLOVE_ERR_INVALID_ARG;
+    const int64_t G = K / 128;
+    const size_t bp = (size_t)M * N * G * 4;
+    if (overlaps(P, bp, A_q, (size_t)M * (K / 2)) || overlaps(P, bp, B_q, (size_t)K * ((N + 1) / 2)) ||
+        overlaps(P, bp, A_zero, (size_t)M * G * 2) || overlaps(P, bp, B_zero, (size_t)G * N * 2))
+        return CLOVE_ERR_ALIASING;
+    DeviceInfo dev;
+    clove_status_t st = current_device_info(&dev);
+    if (st != CLOVE_OK) return st;
+    Int4Args a;
+    a.A = A_q;
+    a.A_zero = static_cast<const uint16_t*>(A_zero);
+    a.B = B_q;
+    a.B_zero = static_cast<const uint16_t*>(B_zero);
+    a.M = M; a.N = N; a.K = K;
+    return launch_i4i4_partials(a, P, dev.num_cus, static_cast<hipStream_t>(stream));
 }
 
 clove_status_t clove_gemm_w4a16(const void* X, const uint8_t* W_q, const void* W_scale,

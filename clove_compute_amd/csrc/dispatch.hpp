@@ -98,6 +98,8 @@ bool try_i4w_int4(const Int4Args& args, int num_cus, hipStream_t stream, clove_s
 // group-wise INT4 x INT4 on int8 MFMA (i4i4_gemm.hip): N >= 64, K % 256 == 0,
 // 16-byte aligned A; zero points in [-112, 127] (others give NaN outputs)
 bool try_i4i4(const Int4Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
+// the int8-MFMA kernel's per-group int32 sums P [M, N, G] (test hook; group-wise)
+clove_status_t launch_i4i4_partials(const Int4Args& args, int32_t* P, int num_cus, hipStream_t stream);
 // SwiGLU of a fused gate/up INT4 weight: args.W holds 2 args.O rows (gate rows,
 // then up rows, scales / zeros likewise), args.Y receives H [T, O]
 bool try_i4w_w4a16_swiglu(const W4A16Args& args, int num_cus, hipStream_t stream, clove_status_t* status);

@@ -44,6 +44,11 @@
 // stages ahead from a three-deep ring, and each wave waits only for its own
 // stream before the workgroup barrier that publishes a stage.
 //
+// Partials mode (PART, the group-partials test hook): each wave stores its
+// group's int32 sums P_g to P [M, N, G] instead of folding them (INT32_MIN
+// where the row's or the column's zero point is outside the exact range), and
+// there is no end phase.
+//
 // End.  Set 1 hands its fp32 sums to set 0 through LDS (fixed order).
 // Split-K over groups when the tiles do not cover the CUs: fp32 partial tiles,
 // the last workgroup to arrive sums them in split order (deterministic).  The
@@ -85,6 +90,7 @@ struct Args {
     int vec_store;        // 16-byte output stores (N % 8 == 0, C 16-byte aligned)
     float* part;
     unsigned* counters;
+    int* P;               // partials mode: [M, N, G] int32
 };
 
 constexpr int NW = 8, NT = 512;
@@ -153,7 +159,8 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Bt[g][n][k'] = int8(qB[k][n] - zB[g][n]) for n < N (0 for N <= n < Npad),
 // k' the unpack order of every 8 k (k0 k2 k4 k6 k1 k3 k5 k7), and
-// sBf[g][n] = sB[g][n] (0 past N; NaN where zB is outside [-112, 127]).
+// sBf[g][n] = sB[g][n] (0 past N, or for a null sB; NaN where zB is outside
+// [-112, 127]).
 // Grid (G, Npad / 64), 128 threads: the group's 128 packed rows of the
 // 64-column slab are staged in LDS with coalesced loads, then thread (p, kq)
 // writes columns 2p, 2p + 1 for k = 32 kq .. 32 kq + 31.
@@ -172,7 +179,7 @@ __global__ void __launch_bounds__(128) i4_prep_bt(const uint8_t* B, int ldb, con
         const int n = 2 * (nb0 + p) + c;
         if (n < N) {
             zh[c] = zB[(int64_t)g * N + n];
-            sh[c] = sB[(int64_t)g * N + n];
+            sh[c] = sB ? sB[(int64_t)g * N + n] : (uint16_t)0;
         }
     }
     // stage: thread t loads 32 bytes of row t (bytes past the row end: 0)
@@ -241,6 +248,7 @@ __global__ void __launch_bounds__(128) i4_prep_bt(const uint8_t* B, int ldb, con
     }
 }
 
+template <bool PART>
 __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
     extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -365,7 +373,7 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
         // wave's slot, its weights as int8 q - z ----
         int z;
         const bool zok = zero_ok((uint16_t)(zw >> half), z);
-        const float sa_row = zok ? h2f((uint16_t)(sw >> half)) : __builtin_nanf("");
+        const float sa_row = zok ? (PART ? 0.0f : h2f((uint16_t)(sw >> half))) : __builtin_nanf("");
         // (both lane halves hold the row: the same value to the same slot)
         *reinterpret_cast<lds_f32*>((size_t)(xs + 4 * m)) = sa_row;
         const unsigned zp = (unsigned)(128 - z) * 0x01010101u;
@@ -391,6 +399,38 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
         // statements fence the fold into this region: its inputs are defined
         // at the start, its results used at the end (otherwise the compiler
         // sinks it to the next group's block, in series with those MFMAs) ----
+        if constexpr (PART) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (s < 2) {
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const int n = ncol0 + 32 * b + m;
+                        bf[b][s + 2] =
+                            bitcast<i32x4>(ld16(sb_st + bbase + n * 128 + 16 * ((4 * h + s + 2) ^ swz(n))));
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    cur[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wq[s], bf[b][s], s == 0 ? i32x16{} : cur[b],
+                                                                   0, 0, 0);
+            }
+            // P[row][col][g]; a NaN row scale (the unpack lane's bad zero
+            // point) or column scale (i4_prep_bt's) marks the sum invalid
+            const int g = gbeg + 2 * t + set;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const int col = n0 + ncol0 + 32 * b + m;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = m0 + 32 * rw + 8 * (i >> 2) + 4 * h + (i & 3);
+                    const float chk = bitcast<float>(scur[i >> 2][i & 3]) + bcur[b];
+                    if (row < M && col < p.N)
+                        p.P[((int64_t)row * p.N + col) * G + g] = chk == chk ? cur[b][i] : (int)0x80000000u;
+                }
+            }
+            return;
+        }
         i32x16 pv[NB];
         f32x16 fa[NB];
 #pragma unroll
@@ -480,6 +520,7 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
     }
     // every DMA has landed and every wave is done with the stages
     dma::stage_barrier<vmcnt_imm(0)>();
+    if constexpr (PART) return;
 
     // ---- set 1 hands its sums to set 0 (LDS, fixed order) ----
     {

@@ -92,6 +92,13 @@ def gemm_int4(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M: int, N: int, K: 
                                           _stream(stream)), "gemm_int4")
 
 
+def gemm_int4_group_acc32(A_q, A_zero, B_q, B_zero, P, M: int, N: int, K: int, stream=None) -> None:
+    """Test hook: the per-group int32 partials P [M, N, K // 128] of group-wise INT4."""
+    _lib.check(_lib.lib().clove_gemm_int4_group_acc32(_ptr(A_q), _ptr(A_zero), _ptr(B_q), _ptr(B_zero),
+                                                      _ptr(P), M, N, K, _stream(stream)),
+               "gemm_int4_group_acc32")
+
+
 def gemm_int4_ex(A_q, A_scale, A_zero, B_q, B_scale, B_zero, C, M: int, N: int, K: int,
                  mode: int = _lib.CLOVE_INT4_GROUPWISE, stream=None) -> None:
     _lib.check(_lib.lib().clove_gemm_int4_ex(_ptr(A_q), _ptr(A_scale), _ptr(A_zero),

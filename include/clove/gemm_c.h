@@ -137,6 +137,22 @@ clove_status_t clove_gemm_int4(const uint8_t* A_q, const void* A_scale,
                                const void* B_scale, const void* B_zero, void* C,
                                int M, int N, int K, void* stream);
 
+/*
+ * Test hook: the per-group int32 partial sums of the group-wise INT4 GEMM,
+ *   P[(m * N + n) * G + g] = sum_{k in group g} (qA[m,k] - zA[m,g]) * (qB[k,n] - zB[g,n])
+ * (G = K / 128), the exact integers the int8-MFMA kernel folds into its fp32
+ * accumulators (same pre-pass, same kernel, no fold), so that they can be
+ * checked bit for bit.  No reference counterpart: the reference's
+ * gemm_int4_kernel never forms per-group partials (src/kernels/gemm_int4.cu:
+ * 137-190 sums every k before scaling).  Operands as clove_gemm_int4 (no
+ * scales).  Domain: K a multiple of 256, A_q 16-byte aligned, P 4-byte aligned
+ * (else CLOVE_ERR_INVALID_ARG); a partial whose row or column zero point lies
+ * outside [-112, 127] is INT32_MIN.
+ */
+clove_status_t clove_gemm_int4_group_acc32(const uint8_t* A_q, const void* A_zero,
+                                           const uint8_t* B_q, const void* B_zero,
+                                           int32_t* P, int M, int N, int K, void* stream);
+
 /* clove_gemm_int4 with an explicit arithmetic mode (see clove_int4_mode_t).
  * In CLOVE_INT4_REFERENCE_LITERAL mode B_q is [K, floor(N/2)] as in the
  * reference and the zero pointers may be NULL (never read). */

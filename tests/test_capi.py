@@ -107,6 +107,19 @@ def test_int4_validation(L):
     assert g(A, S, None, B, BS, None, C, 4, 4, 7, lit, None) == _lib.CLOVE_ERR_INVALID_ARG
 
 
+def test_int4_group_acc32_validation(L):
+    Z, BZ, P = 0x500000, 0x700000, 0x800000
+    f = L.clove_gemm_int4_group_acc32
+    assert f(A, Z, B, BZ, P, 4, 4, 128, None) == _lib.CLOVE_ERR_INVALID_ARG  # K not a multiple of 256
+    assert f(A + 8, Z, B, BZ, P, 4, 4, 256, None) == _lib.CLOVE_ERR_INVALID_ARG  # A not 16-byte aligned
+    assert f(A, Z, B, BZ, P + 2, 4, 4, 256, None) == _lib.CLOVE_ERR_INVALID_ARG
+    assert f(A, Z, B, BZ, P, 4, -4, 256, None) == _lib.CLOVE_ERR_INVALID_DIM
+    assert f(A, None, B, BZ, P, 4, 4, 256, None) == _lib.CLOVE_ERR_NULL_POINTER
+    assert f(A, Z, B, BZ, None, 4, 4, 256, None) == _lib.CLOVE_ERR_NULL_POINTER
+    assert f(A, Z, B, BZ, Z, 4, 4, 256, None) == _lib.CLOVE_ERR_ALIASING
+    assert f(A, Z, B, BZ, P, 0, 4, 256, None) == _lib.CLOVE_OK
+
+
 def test_w4a16_validation(L):
     W, S, Z = 0x400000, 0x500000, 0x600000
     f = L.clove_gemm_w4a16

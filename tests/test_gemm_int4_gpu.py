@@ -226,3 +226,68 @@ def test_int8_mfma_path_split_k(M, N, K):
     _, ref, _ = oracle.gemm_int4_groupwise(A_q[rows], sA[rows], zA[rows], B_q, sB, zB, len(rows), N, K)
     ok, rep = within_tol(C[rows], ref)
     assert ok, rep
+
+
+def run_group_acc32(A_q, zA, B_q, zB, M, N, K):
+    import torch
+    G = K // 128
+    P = torch.full((M, N, G), 12345, dtype=torch.int32, device="cuda")
+    _cg().gemm_int4_group_acc32(to_dev(A_q), to_dev(zA), to_dev(B_q), to_dev(zB), P, M, N, K)
+    torch.cuda.synchronize()
+    return P.cpu().numpy()
+
+
+def partials_int64(A_q, zA, B_q, zB, rows, N, K):
+    # independent restatement: unpack with numpy, int64 sums per group
+    qA = quant.unpack_rows(A_q[rows], K).astype(np.int64)           # [r, K]
+    qB = quant.unpack_cols(B_q, N).astype(np.int64)                 # [K, N]
+    G = K // 128
+    za = np.rint(zA[rows].astype(np.float64)).astype(np.int64)     # [r, G]
+    zb = np.rint(zB.astype(np.float64)).astype(np.int64)           # [G, N]
+    a = (qA.reshape(len(rows), G, 128) - za[:, :, None])           # [r, G, 128]
+    b = (qB.reshape(G, 128, N) - zb[:, None, :])                   # [G, 128, N]
+    return np.einsum("rgk,gkn->rng", a, b)
+
+
+# The int8-MFMA kernel's per-group integer sums P_g, through the partials hook:
+# bit for bit against the oracle's partials and an independent numpy int64
+# restatement, with arbitrary zero points over the kernel's whole exact range
+# [-112, 127] (not only 8) and ragged M / N.
+@pytest.mark.parametrize("M,N,K", [(130, 64, 512), (64, 1, 256), (257, 200, 1024), (1000, 128, 11008)])
+def test_group_partials_bit_exact(M, N, K):
+    g = rng("i4-partials", M, N, K)
+    G = K // 128
+    A_q = quant.pack_rows(g.integers(0, 16, (M, K)))
+    B_q = quant.pack_cols(g.integers(0, 16, (K, N)))
+    zA = g.integers(-112, 128, (M, G)).astype(np.float16)
+    zB = g.integers(-112, 128, (G, N)).astype(np.float16)
+    P = run_group_acc32(A_q, zA, B_q, zB, M, N, K)
+    rows = np.arange(M) if M <= 300 else np.unique(np.concatenate([[0, 63, 64, M - 1], g.integers(0, M, 24)]))
+    ref = partials_int64(A_q, zA, B_q, zB, rows, N, K)
+    assert np.array_equal(P[rows].astype(np.int64), ref)
+    if M <= 300:
+        sA = np.ones((M, G), np.float16)
+        sB = np.ones((G, N), np.float16)
+        _, _, part = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K, want_partials=True)
+        assert np.array_equal(P, part)
+
+
+def test_group_partials_zero_point_outside_range():
+    # a zero point the int8 operands cannot hold marks exactly the partials of
+    # its row (or column) and group with INT32_MIN
+    M, N, K = 70, 90, 512
+    g = rng("i4-partials-bad", M, N, K)
+    G = K // 128
+    A_q = quant.pack_rows(g.integers(0, 16, (M, K)))
+    B_q = quant.pack_cols(g.integers(0, 16, (K, N)))
+    zA = g.integers(0, 16, (M, G)).astype(np.float16)
+    zB = g.integers(0, 16, (G, N)).astype(np.float16)
+    zA[3, 1] = 130.0
+    zB[2, 40] = -113.0
+    P = run_group_acc32(A_q, zA, B_q, zB, M, N, K)
+    bad = np.zeros((M, N, G), bool)
+    bad[3, :, 1] = True
+    bad[:, 40, 2] = True
+    assert np.all(P[bad] == np.iinfo(np.int32).min)
+    ref = partials_int64(A_q, zA, B_q, zB, np.arange(M), N, K)
+    assert np.array_equal(P[~bad].astype(np.int64), ref[~bad])
