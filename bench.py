@@ -551,6 +551,13 @@ def main():
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
+    # leave nothing behind on the GPU: the library's split-K scratch is freed and
+    # every stream drained before the interpreter tears the runtime down
+    import torch
+    import clove_compute_amd as cg
+    torch.cuda.synchronize()
+    cg.release_scratch()
+    torch.cuda.empty_cache()
 
 
 if __name__ == "__main__":

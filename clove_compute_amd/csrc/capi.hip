@@ -74,6 +74,25 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
+}  // namespace
+
+clove_status_t ensure_lds(const void* kernel, int bytes) {
+    if (bytes <= 64 * 1024) return CLOVE_OK;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return CLOVE_ERR_NO_DEVICE;
+    static std::mutex mu;
+    static std::vector<std::tuple<int, const void*, int>> done;  // (device, kernel, bytes set)
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& e : done)
+        if (std::get<0>(e) == dev && std::get<1>(e) == kernel && std::get<2>(e) >= bytes) return CLOVE_OK;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+        return CLOVE_ERR_LAUNCH;
+    done.emplace_back(dev, kernel, bytes);
+    return CLOVE_OK;
+}
+
+namespace {
+
 // ---------------------------------------------------------------------------
 // caller-owned workspace (clove_workspace_bind / clove_workspace_query_*), per
 // host thread.  Layout of a bound workspace: the completion counters at its

@@ -142,4 +142,9 @@ inline clove_status_t check_launch() {
     return hipGetLastError() == hipSuccess ? CLOVE_OK : CLOVE_ERR_LAUNCH;
 }
 
+// Raises a kernel's dynamic-LDS limit to `bytes` (needed above 64 KB) once per
+// (device, kernel): the setting is per device and lasts for the process, so
+// later calls only look it up.
+clove_status_t ensure_lds(const void* kernel, int bytes);
+
 }  // namespace clove

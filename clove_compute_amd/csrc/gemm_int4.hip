@@ -360,10 +360,7 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
     wpb = min(wpb, (aligned ? gemv_max_threads<NV, true, 4>() : gemv_max_threads<NV, false, 4>()) / 64);
     const dim3 grid(cdiv(p.M, wpb * RPW));
     auto k = aligned ? int4_gemv<NV, MODE, RPW, UPR, true> : int4_gemv<NV, MODE, RPW, UPR, false>;
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-        return CLOVE_ERR_LAUNCH;
+    if (ensure_lds(reinterpret_cast<const void*>(k), (int)lds) != CLOVE_OK) return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
 }

@@ -78,8 +78,7 @@ clove_status_t run(const Int4Args& q, int32_t* P, int cus, hipStream_t stream) {
     CLOVE_LAUNCH(i4_prep_bt, dim3((unsigned)G, (unsigned)(Npad / PREP_COLS)), dim3(128), 0, stream, q.B, ldb,
                  P ? nullptr : q.B_scale, q.B_zero, q.N, q.K, Npad, bt, sbf);
     auto k = P ? i4i4_gemm<true> : i4i4_gemm<false>;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, LDS) !=
-        hipSuccess)
+    if (ensure_lds(reinterpret_cast<const void*>(k), LDS) != CLOVE_OK)
         return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, dim3((unsigned)(tiles * a.nsplit)), dim3(NT), LDS, stream, a);
     return check_launch();

@@ -65,9 +65,7 @@ clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_byt
     auto k = i4w_gemm<CF, XS, OUT>;
     constexpr int lds = CF::template lds_bytes<XS>();
     static_assert(lds <= 160 * 1024, "LDS");
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            lds) != hipSuccess)
+    if (ensure_lds(reinterpret_cast<const void*>(k), lds) != CLOVE_OK)
         return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, dim3((unsigned)(tiles * pl.nsplit)), dim3(CF::NT), lds, stream, a);
     return check_launch();
@@ -99,9 +97,7 @@ clove_status_t launch_stream(const Args& a, hipStream_t stream) {
     using SC = SCfg<WF, XF, NG, KS>;
     const int lds = SC::lds_bytes(a.G, XS, RAWB);
     auto k = i4w_stream<SC, XS, OUT, RAWB>;
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, lds) !=
-            hipSuccess)
+    if (ensure_lds(reinterpret_cast<const void*>(k), lds) != CLOVE_OK)
         return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, dim3((unsigned)cdiv(a.R, SC::ROWS)), dim3(SC::NT), lds, stream, a);
     return check_launch();

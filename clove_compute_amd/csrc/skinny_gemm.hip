@@ -50,9 +50,7 @@ clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
         a.counters = s.counters;
     }
     auto k = skinny_gemm<CF, OUT>;
-    if (CF::LDS > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            CF::LDS) != hipSuccess)
+    if (ensure_lds(reinterpret_cast<const void*>(k), CF::LDS) != CLOVE_OK)
         return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, dim3((unsigned)(tiles * a.nsplit)), dim3(CF::NT), CF::LDS, stream, a);
     return check_launch();

@@ -146,15 +146,27 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
     const int wm = wave % CF::WM, wn = wave / CF::WM;
 
     // ---- tile, split, K range ----
-    // split-major order: the workgroups in flight together share K rows of B
-    // (whole rows of N are read at once, which keeps HBM pages open)
+    // Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD
+    // b % 8) and each XCD has its own L2: the grid is renumbered so that every
+    // XCD owns a contiguous run of logical workgroups.  Logical order is
+    // split-major (the workgroups in flight together share K rows of B), and
+    // within a split the tiles are walked in groups of 8 tile-rows, column by
+    // column, so one XCD's run shares a few A row panels and B column panels
+    // instead of touching every A panel.
+    int bid = blockIdx.x;
+    if ((gridDim.x & 7) == 0) bid = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);
     const int ntiles = p.tiles_m * p.tiles_n * p.batch;
-    const int split = blockIdx.x / ntiles;
-    int tile = blockIdx.x - split * ntiles;
+    const int split = bid / ntiles;
+    int tile = bid - split * ntiles;
     const int per_batch = p.tiles_m * p.tiles_n;
     const int batch = tile / per_batch;
     const int t_in = tile - batch * per_batch;
-    const int tn = t_in % p.tiles_n, tm = t_in / p.tiles_n;
+    constexpr int GM = 8;
+    const int group = t_in / (GM * p.tiles_n);
+    const int first_m = group * GM;
+    const int gm = min(p.tiles_m - first_m, GM);
+    const int in_group = t_in - group * GM * p.tiles_n;
+    const int tm = first_m + in_group % gm, tn = in_group / gm;
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.M, N = p.N, K = p.K;
     const int kbeg = split * p.kps;

@@ -283,10 +283,7 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
     wpb = min(wpb, (aligned ? w4_max_threads<TV, RPW, UPR, true>() : w4_max_threads<TV, RPW, UPR, false>()) / 64);
     const dim3 grid(cdiv(p.O, wpb * (SWIGLU ? RPW / 2 : RPW)));
     auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true, SWIGLU> : w4a16_gemv<TV, RPW, UPR, false, SWIGLU>;
-    if (lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-        return CLOVE_ERR_LAUNCH;
+    if (ensure_lds(reinterpret_cast<const void*>(k), (int)lds) != CLOVE_OK) return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
 }
