@@ -487,6 +487,28 @@ def floor():
                      "GBs_hot": round(nbytes / hot / 1e3, 1)}
         print(f"[floor] {name}: cold {us:.2f} us, hot {hot:.2f} us", file=sys.stderr, flush=True)
         del bufs, calls
+    # one CU's pull rate: 32 workgroups, each streaming 1 MB of a 32 MB buffer
+    # (at most one workgroup per CU) with 32 KB or 128 KB in flight, cold and hot
+    lib.clove_diag_stream_read_chunked.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                                   ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.clove_diag_stream_read_chunked.restype = ctypes.c_int
+    nbytes, chunk = 32 << 20, 1 << 20
+    bufs = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(copies_for(nbytes))]
+    for depth in (1, 4):
+        def call_chunk(b, depth=depth):
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            if lib.clove_diag_stream_read_chunked(b.data_ptr(), nbytes, chunk, depth, sink.data_ptr(), stream) <= 0:
+                raise RuntimeError("clove_diag_stream_read_chunked failed")
+        calls = [lambda b=b: call_chunk(b) for b in bufs]
+        us = graph_time(calls, [], 5)
+        hot = graph_time(calls[:1] * 16, [], 5)
+        out[f"per_cu_32x1MB_inflight_{32 * depth}KB"] = {
+            "workgroups": nbytes // chunk, "MB_per_workgroup": 1.049, "us_cold": round(us, 3),
+            "GBs_per_workgroup_cold": round(chunk / us / 1e3, 1), "us_hot": round(hot, 3),
+            "GBs_per_workgroup_hot": round(chunk / hot / 1e3, 1)}
+        print(f"[floor] per CU (32 x 1 MB, {32 * depth} KB in flight): cold {us:.2f} us, hot {hot:.2f} us",
+              file=sys.stderr, flush=True)
+    del bufs, calls
     print(json.dumps({"floor": out, "device": device_info()}), flush=True)
 
 

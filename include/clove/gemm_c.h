@@ -191,9 +191,11 @@ clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int 
  * input [batch_seq, hidden_dim], W_gate / W_up [hidden_dim, intermediate_dim]
  * (gemm_fp16's B layout), output [batch_seq, intermediate_dim], all fp16.
  * Replaces clove::swiglu_fused, declared in include/clove/kernels/
- * activations.cuh:37-46 and never defined there.  Runs the two FP16 GEMMs
- * (the up projection into a library-owned buffer per stream, kept like the
- * split-K scratch) and the SwiGLU pass.
+ * activations.cuh:37-46 and never defined there.  One launch that writes
+ * neither projection to memory: each output tile's gate and up sums are
+ * formed side by side (the same k order as two separate gemm_fp16 calls, so
+ * the result equals gemm_fp16 x 2 followed by clove_swiglu bit for bit) and
+ * the epilogue applies SwiGLU to their fp16 values.
  */
 clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const void* W_up,
                                   void* output, int batch_seq, int hidden_dim,
@@ -221,7 +223,11 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
  *  - a bound workspace, clove_workspace_bind(ptr, bytes): calls on this thread
  *    take their split-K partials, completion counters and intermediates from
  *    [ptr, ptr + bytes) and allocate nothing; a call that needs more returns
- *    CLOVE_ERR_WORKSPACE and launches nothing.  ptr must be 256-byte aligned
+ *    CLOVE_ERR_WORKSPACE and launches nothing.  (One exception: the GEMV
+ *    variants for operands that are not 16-byte aligned -- INT4 with N <= 8 and
+ *    W4A16 with T <= 4 -- spill registers to private scratch, which the HIP
+ *    runtime sizes on their first launch; every kernel an aligned call
+ *    reaches uses none, which the library build checks.)  ptr must be 256-byte aligned
  *    and bytes >= CLOVE_WORKSPACE_MIN_BYTES; the first CLOVE_WORKSPACE_MIN_BYTES
  *    (the counters) must be zero before the first call, and every call leaves
  *    them zero.  Calls that may run at the same time on the device (other
