@@ -508,6 +508,25 @@ def floor():
             "GBs_per_workgroup_hot": round(chunk / hot / 1e3, 1)}
         print(f"[floor] per CU (32 x 1 MB, {32 * depth} KB in flight): cold {us:.2f} us, hot {hot:.2f} us",
               file=sys.stderr, flush=True)
+    # the same pull by load kind: 32 workgroups on their own 1 MB (cold, the
+    # copies rotated), and 256 workgroups (one per CU) all reading one 1 MB
+    # chunk that then sits in every XCD's L2
+    lib.clove_diag_pull.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    lib.clove_diag_pull.restype = ctypes.c_int
+    for kind, kname in ((0, "nontemporal"), (1, "cached"), (2, "lds_dma")):
+        for shared, grid in ((0, nbytes // chunk), (1, 256)):
+            def call_pull(b, kind=kind, shared=shared, grid=grid):
+                stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                if lib.clove_diag_pull(b.data_ptr(), chunk, grid, shared, kind, sink.data_ptr(), stream) != grid:
+                    raise RuntimeError("clove_diag_pull failed")
+            calls = [lambda b=b: call_pull(b) for b in bufs]
+            us = graph_time(calls if not shared else calls[:1] * 16, [], 5)
+            key = f"pull_{kname}_{'l2_shared_256x1MB' if shared else 'cold_32x1MB'}"
+            out[key] = {"workgroups": grid, "us": round(us, 3), "GBs_per_workgroup": round(chunk / us / 1e3, 1),
+                        "GBs_total": round(grid * chunk / us / 1e3, 1)}
+            print(f"[floor] {key}: {us:.2f} us, {chunk / us / 1e3:.1f} GB/s per workgroup",
+                  file=sys.stderr, flush=True)
     del bufs, calls
     print(json.dumps({"floor": out, "device": device_info()}), flush=True)
 

@@ -256,10 +256,12 @@ def test_skinny_small_integers_bit_exact(M, N, K):
     assert np.array_equal(f16bits(C), f16bits(ref))
 
 
-# M = 2..4 on the GEMV with several K splits (K > 256): the per-row partials,
-# split publication and reduce of every row count, beta != 0; small integers
-# make every order exact, so the comparison is bit for bit
-@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 1024, 2048), (4, 1024, 2048)])
+# M = 1..4 on the GEMV with several K splits (K > 256), ragged last splits
+# (8200, 11008, 4104) and a half column block (1032, 4104, 136): the per-row
+# partials, split publication and reduce of every row count, beta != 0; small
+# integers make every order exact, so the comparison is bit for bit
+@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 1024, 2048), (4, 1024, 2048), (2, 1032, 8200),
+                                   (1, 4104, 11008), (4, 136, 4104)])
 def test_gemv_multirow_split_k_bit_exact(M, N, K):
     g = rng("gemv-mm", M, N, K)
     A = g.integers(-3, 4, (M, K)).astype(np.float16)
