@@ -10,7 +10,6 @@ using namespace sk;
 
 // (I8, BM, BN, WM, WN, stages)
 using F16M32 = Cfg<false, 32, 128, 1, 4, 5>;
-using F16M64 = Cfg<false, 64, 128, 2, 2, 4>;
 using F16M128 = Cfg<false, 128, 64, 4, 1, 4>;
 // mid-size shapes (M > 256) whose 256x256 tile grid would leave CUs idle:
 // 128x128 tiles (waves of 64x64), or 64x64 tiles when even those are too few
@@ -21,7 +20,6 @@ using F16M128 = Cfg<false, 128, 64, 4, 1, 4>;
 using F16T128 = Cfg<false, 128, 128, 2, 2, 3>;
 using F16T64 = Cfg<false, 64, 64, 2, 2, 6>;
 using I8M32 = Cfg<true, 32, 128, 1, 4, 5>;
-using I8M64 = Cfg<true, 64, 128, 2, 2, 4>;
 using I8M128 = Cfg<true, 128, 64, 4, 1, 4>;
 
 template <class CF, int OUT>
@@ -61,19 +59,20 @@ bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 // The FP16 tile shapes, chosen by shape alone (so that the fused SwiGLU below
 // picks the same tiles, and with them the same split plan, as the two GEMMs
 // it replaces).
-enum class F16Tile { kM32, kM64, kM128, kT128, kT64 };
+enum class F16Tile { kM32, kM128, kT128, kT64 };
 
 F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
     if (M > 256) {
         const int64_t t128 = (int64_t)cdiv(M, 128) * cdiv(N, 128) * batch;
         return t128 >= cus / 2 ? F16Tile::kT128 : F16Tile::kT64;
     }
-    // short K with few 128-row tiles: the 32-row tiles make 4x the workgroups
+    // 32-row tiles up to M = 64 (cold 4096 x 4096 weights: M = 40 / 48 / 64 at
+    // 13.6 / 14.1 / 14.5 us against 14.9 / 15.3 / 15.5 with 64-row tiles), and
+    // for short K with few 128-row tiles, where they make 4x the workgroups
     // without a split (512^3: 6.1 us against 7.2, measured)
     const bool short_k = K <= 16 * F16M128::BK &&
                          (int64_t)cdiv(M, F16M128::BM) * cdiv(N, F16M128::BN) * batch < cus / 2;
-    if (M <= 32 || (M > 64 && short_k)) return F16Tile::kM32;
-    if (M <= 64) return F16Tile::kM64;
+    if (M <= 64 || short_k) return F16Tile::kM32;
     return F16Tile::kM128;
 }
 
@@ -87,7 +86,6 @@ bool f16_domain(const void* A, const void* B, const void* C, int M, int N, int K
 // two-B-operand (gate, up) counterparts of the tiles above; fewer stages
 // where both B tiles would not fit the LDS
 using SwM32 = Cfg<false, 32, 128, 1, 4, 4, 2>;
-using SwM64 = Cfg<false, 64, 128, 2, 2, 4, 2>;
 using SwM128 = Cfg<false, 128, 64, 4, 1, 4, 2>;
 using SwT128 = Cfg<false, 128, 128, 2, 2, 3, 2>;
 using SwT64 = Cfg<false, 64, 64, 2, 2, 6, 2>;
@@ -111,7 +109,6 @@ bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batc
     a.sC = (int64_t)M * N;
     switch (pick_f16_tile(batch, M, N, K, cus)) {
         case F16Tile::kM32: *status = run<F16M32, kF16AlphaBeta>(a, batch, cus, stream); break;
-        case F16Tile::kM64: *status = run<F16M64, kF16AlphaBeta>(a, batch, cus, stream); break;
         case F16Tile::kM128: *status = run<F16M128, kF16AlphaBeta>(a, batch, cus, stream); break;
         case F16Tile::kT128: *status = run<F16T128, kF16AlphaBeta>(a, batch, cus, stream); break;
         case F16Tile::kT64: *status = run<F16T64, kF16AlphaBeta>(a, batch, cus, stream); break;
@@ -136,7 +133,6 @@ bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t
     a.sC = (int64_t)T * inter;
     switch (pick_f16_tile(1, T, inter, hidden, cus)) {
         case F16Tile::kM32: *status = run<SwM32, kF16SwiGLU>(a, 1, cus, stream); break;
-        case F16Tile::kM64: *status = run<SwM64, kF16SwiGLU>(a, 1, cus, stream); break;
         case F16Tile::kM128: *status = run<SwM128, kF16SwiGLU>(a, 1, cus, stream); break;
         case F16Tile::kT128: *status = run<SwT128, kF16SwiGLU>(a, 1, cus, stream); break;
         case F16Tile::kT64: *status = run<SwT64, kF16SwiGLU>(a, 1, cus, stream); break;
@@ -161,11 +157,12 @@ bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_statu
     a.K = q.K;
     auto pick = [&](auto out_tag) -> clove_status_t {
         constexpr int OUT = decltype(out_tag)::value;
-        // as for FP16: short K with few 128-row tiles takes the 32-row tiles
+        // 32-row tiles up to M = 128 (cold 4096 x 4096 weights: M = 64 / 128 at
+        // 10.8 / 13.8 us against 15.0 / 15.3 with 64- and 128-row tiles; from
+        // M = 160 the 128-row tiles are ahead), and for short K as for FP16
         const bool short_k = q.K <= 16 * I8M128::BK &&
                              (int64_t)cdiv(q.M, I8M128::BM) * cdiv(q.N, I8M128::BN) < cus / 2;
-        if (q.M <= 32 || (q.M > 64 && short_k)) return run<I8M32, OUT>(a, 1, cus, stream);
-        if (q.M <= 64) return run<I8M64, OUT>(a, 1, cus, stream);
+        if (q.M <= 128 || short_k) return run<I8M32, OUT>(a, 1, cus, stream);
         return run<I8M128, OUT>(a, 1, cus, stream);
     };
     switch (q.out) {

@@ -186,7 +186,7 @@ def test_w4a16_swiglu_equals_layers_then_swiglu():
 # ---- FP16 swiglu_fused (the reference's declaration) ----
 # One launch, no intermediate: the FP16 GEMV with two weight operands for
 # T <= 4, the skinny MFMA kernel with two B operands for T > 4 (every tile
-# shape: 32x128, 64x128, 128x64, 64x64, 128x128 with and without K splits),
+# shape: 32x128, 128x64, 64x64, 128x128 with and without K splits),
 # and the direct fallback for unaligned operands or hidden % 64 != 0.
 
 def run_swiglu_fused(X, Wg, Wu, offset=False):
