@@ -407,6 +407,31 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
         for (int q = 0; q < 16; ++q) s += red[q][m][col];
         sum[m] = s;
     }
+    if (p.nsplit > 1 && p.ws == nullptr) {
+        // one round trip: every split adds (1 << 48) + (sum + 2^31) to the
+        // output's 64-bit word in the zeroed counter region with one
+        // device-scope atomic; the split whose returned count is nsplit - 1
+        // holds the whole exact integer sum (the low 48 bits, less nsplit 2^31),
+        // stores the output and re-arms the word to zero for the next launch
+        if (!active || gn >= N) return;
+        const float cs = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sb[gn]) : 1.0f;
+        uint64_t* acc64 = reinterpret_cast<uint64_t*>(p.counters) + (int64_t)cb * MM * IV_COLS + col;
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            if (m >= M) break;
+            const float rs = OUT == (int)Int8Out::kHalfRowCol ? h2f(p.sa[m]) : 1.0f;
+            constexpr uint64_t kLow = ((uint64_t)1 << 48) - 1;
+            const uint64_t add = ((uint64_t)1 << 48) | (uint64_t)((int64_t)sum[m] + 0x80000000ll);
+            const uint64_t old = __hip_atomic_fetch_add(acc64 + m * IV_COLS, add, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+            if ((old >> 48) == (uint64_t)(p.nsplit - 1)) {
+                const int64_t tot = (int64_t)((old & kLow) + (add & kLow)) - (int64_t)p.nsplit * 0x80000000ll;
+                __hip_atomic_store(acc64 + m * IV_COLS, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                int8_store<OUT>(p, m, gn, (int)(uint32_t)(uint64_t)tot, rs * cs);
+            }
+        }
+        return;
+    }
     if (p.nsplit > 1) {
         float* ws_tile = p.ws + (int64_t)cb * p.nsplit * (MM * IV_COLS);
         if (active) {
@@ -461,13 +486,25 @@ clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     const int rows = mm == 1 ? iv_rows<1>() : (mm == 2 ? iv_rows<2>() : iv_rows<4>());
     p.nsplit = cdiv(p.K, rows);
     p.k_per_split = rows;
+    p.ws = nullptr;
+    p.counters = nullptr;
     if (p.nsplit > 1) {
+        // the one-round-trip reduction needs one zeroed 64-bit word per output
+        // (mm x 256 per column block) in the counter region; a bound workspace
+        // whose counter region is smaller takes the partial-tile reduction
         Scratch s;
-        clove_status_t st = acquire_scratch(stream, (size_t)col_blocks * p.nsplit * mm * IV_COLS * 4,
-                                            (size_t)col_blocks, &s);
-        if (st != CLOVE_OK) return st;
-        p.ws = s.partials;
-        p.counters = s.counters;
+        clove_status_t st = CLOVE_ERR_WORKSPACE;
+        if (p.nsplit < 65536) st = acquire_scratch(stream, 0, (size_t)col_blocks * mm * IV_COLS * 2, &s);
+        if (st == CLOVE_OK) {
+            p.counters = s.counters;
+        } else if (st == CLOVE_ERR_WORKSPACE) {
+            st = acquire_scratch(stream, (size_t)col_blocks * p.nsplit * mm * IV_COLS * 4, (size_t)col_blocks, &s);
+            if (st != CLOVE_OK) return st;
+            p.ws = s.partials;
+            p.counters = s.counters;
+        } else {
+            return st;
+        }
     }
     const int64_t g = (int64_t)col_blocks * p.nsplit;
     if (g > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
