@@ -304,35 +304,39 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV (M <= 4): 1024 threads = 16 column lanes x 64 K lanes; a column lane
-// owns 16 consecutive columns (one 16-byte load per K row).
+// GEMV (M <= 4): 1024 threads = CL column lanes x (1024 / CL) K lanes; a
+// column lane owns 16 consecutive columns (one 16-byte load per K row).
 // ---------------------------------------------------------------------------
-// A workgroup of 1024 threads owns 256 columns x 512 k-rows of B: thread
-// (kl, cl) = (tid / 16, tid % 16) loads the 16 bytes of columns 16cl..16cl+15
-// of rows kl + 64j, j < 8, so each wave instruction reads four full 256-byte
-// row segments and the whole 128 KB tile is requested at once (4096 x 4096:
-// 9.8 us with 256-row tiles, 9.2 with 512, 11.8 with 1024, measured).  Loads are
-// unconditional from clamped addresses (masked at use).  int32 partials:
-// within a wave (4 k lanes, by v_permlane row swaps), across the 16 waves
-// through LDS, then across the K splits by the last workgroup to arrive
-// (split order).
-// With 4 output rows the accumulators (64) and 8 rows of B in flight (32)
-// exceed the 128 VGPRs of a 1024-thread workgroup, so MM = 4 takes 4 rows per
-// thread (a 256-row tile, twice the K splits) and runs without scratch.
-constexpr int IV_COLS = 256;
-constexpr int IV_KL = 64;
+// A workgroup owns 16 CL columns x 512 k-rows of B (MM <= 2: 128 columns, 8
+// column lanes, 128 k lanes) or 256 columns x 256 k-rows (MM = 4: 16 column
+// lanes, 64 k lanes; 4 output rows of accumulators beside 8 rows of B in
+// flight would exceed the 128 VGPRs of a 1024-thread workgroup): thread
+// (kl, cl) loads the 16 bytes of columns 16cl..16cl+15 of rows kl + KL j,
+// j < 4, so each wave instruction reads whole 128- or 256-byte row segments
+// and the workgroup's 64 KB tile is requested at once (4096 x 4096, M = 1:
+// 256 workgroups; 7.9 us against 8.2 with 256 columns x 512 rows and 9.8 with
+// 256 x 256, measured with the partial-tile reduction; M = 4 at 128 columns
+// and two rows per thread took 21.7 us against 13.9).  Loads are
+// unconditional from clamped addresses (masked at use).  int32 sums: within a
+// wave (DPP and v_permlane row swaps), across the 16 waves through LDS, then
+// across the K splits (one round trip, see the end of the kernel).
 template <int MM>
-constexpr int iv_rpt() { return MM >= 4 ? 4 : 8; }
+constexpr int iv_cols() { return MM >= 4 ? 256 : 128; }
 template <int MM>
-constexpr int iv_rows() { return IV_KL * iv_rpt<MM>(); }
+constexpr int iv_kl() { return 1024 / (iv_cols<MM>() / 16); }
+template <int MM>
+constexpr int iv_rpt() { return 4; }
+template <int MM>
+constexpr int iv_rows() { return iv_kl<MM>() * iv_rpt<MM>(); }
 
 template <int MM, int OUT>
 __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
     constexpr int IV_RPT = iv_rpt<MM>(), IV_ROWS = iv_rows<MM>();
+    constexpr int IV_COLS = iv_cols<MM>(), IV_KL = iv_kl<MM>(), CL = IV_COLS / 16;  // CL: column lanes
     __shared__ int red[16][MM][IV_COLS];
     __shared__ int s_last;
     const int tid = threadIdx.x;
-    const int cl = tid & 15, kl = tid >> 4, wave = tid >> 6, lane = tid & 63;
+    const int cl = tid % CL, kl = tid / CL, wave = tid >> 6, lane = tid & 63;
     const int split = blockIdx.x % p.nsplit;
     const int cb = blockIdx.x / p.nsplit;
     const int M = p.M, N = p.N, K = p.K;
@@ -384,14 +388,24 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
                 for (int m = 0; m < MC; ++m) acc[m][e] += __mul24(a[m], b);
             }
         }
-        // the four k lanes of a column lane (l, l+16, l+32, l+48) by row
-        // swaps: lane l of row r ends with column 16 cl + 4 u + r, u < 4
+        // the k lanes of a column lane: with 8 column lanes first lanes l and
+        // l ^ 8 (a DPP rotation by 8 within each 16-lane row), then (l, l+16,
+        // l+32, l+48) by row swaps: lane l of row r ends with column
+        // 16 cl + 4 u + r, u < 4 (with 8 column lanes, lanes l and l ^ 8 hold
+        // the same sums and the one with bit 3 clear writes them)
+        if constexpr (CL == 8) {
+#pragma unroll
+            for (int m = 0; m < MC; ++m)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[m][e] += __builtin_amdgcn_mov_dpp(acc[m][e], 0x128, 0xf, 0xf, false);
+        }
 #pragma unroll
         for (int m = 0; m < MC; ++m)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                red[wave][m0 + m][cl * 16 + 4 * u + (lane >> 4)] =
-                    rows_sum4(acc[m][4 * u], acc[m][4 * u + 1], acc[m][4 * u + 2], acc[m][4 * u + 3]);
+            for (int u = 0; u < 4; ++u) {
+                const int v = rows_sum4(acc[m][4 * u], acc[m][4 * u + 1], acc[m][4 * u + 2], acc[m][4 * u + 3]);
+                if (CL == 16 || (lane & 8) == 0) red[wave][m0 + m][cl * 16 + 4 * u + (lane >> 4)] = v;
+            }
     }
     __syncthreads();
     // threads 0..255 own one column each from here on; every thread still
@@ -481,9 +495,10 @@ namespace {
 
 template <int OUT>
 clove_status_t run_gemv(I8Params p, hipStream_t stream) {
-    const int col_blocks = cdiv(p.N, IV_COLS);
     const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
     const int rows = mm == 1 ? iv_rows<1>() : (mm == 2 ? iv_rows<2>() : iv_rows<4>());
+    const int IV_COLS = mm == 4 ? iv_cols<4>() : iv_cols<1>();
+    const int col_blocks = cdiv(p.N, IV_COLS);
     p.nsplit = cdiv(p.K, rows);
     p.k_per_split = rows;
     p.ws = nullptr;
