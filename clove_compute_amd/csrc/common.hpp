@@ -93,6 +93,26 @@ __device__ __forceinline__ T halves_sum2(T x, T y) {
     return swap_sum32(x, y);
 }
 
+// One register summed over all 64 lanes, every lane returning the total,
+// without the LDS pipe: inside each 16-lane row DPP row_ror:8 (lane l ^ 8),
+// row_ror:4 (with the step before, the 4 lanes of l's class mod 4) and the
+// quad_perm swaps [2,3,0,1] (l ^ 2) and [1,0,3,2] (l ^ 1) leave the row's
+// sum in every lane of the row; the four row sums are read into scalars and
+// added as (row 0 + row 1) + (row 2 + row 3).  A fixed order (the same bits
+// on every call), and one extra register per value.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+    v = v + bitcast<T>(__builtin_amdgcn_mov_dpp(bitcast<int>(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+    v = v + bitcast<T>(__builtin_amdgcn_mov_dpp(bitcast<int>(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+    v = v + bitcast<T>(__builtin_amdgcn_mov_dpp(bitcast<int>(v), 0x4e, 0xf, 0xf, false));   // quad_perm 2301
+    v = v + bitcast<T>(__builtin_amdgcn_mov_dpp(bitcast<int>(v), 0xb1, 0xf, 0xf, false));   // quad_perm 1032
+    const T r0 = bitcast<T>(__builtin_amdgcn_readlane(bitcast<int>(v), 0));
+    const T r1 = bitcast<T>(__builtin_amdgcn_readlane(bitcast<int>(v), 16));
+    const T r2 = bitcast<T>(__builtin_amdgcn_readlane(bitcast<int>(v), 32));
+    const T r3 = bitcast<T>(__builtin_amdgcn_readlane(bitcast<int>(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // Streaming GEMVs with V weight columns (or token rows): the wide variants
 // (V >= WIDE) and the byte-gathering unaligned ones need more than the 128
 // VGPRs a 1024-thread workgroup leaves, so they run with at most 512 threads

@@ -285,17 +285,14 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
         }
     }
 
-    // ---- reduce over the wave (fixed butterfly order) ----
+    // ---- reduce over the wave (a fixed butterfly, permlane swaps and DPP) ----
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int n = 0; n < NV; ++n) {
-                if constexpr (MODE == mg::kI4Groupwise) accf[r][n] += __shfl_xor(accf[r][n], off);
-                else acci[r][n] += __shfl_xor(acci[r][n], off);
-            }
-    }
+        for (int n = 0; n < NV; ++n) {
+            if constexpr (MODE == mg::kI4Groupwise) accf[r][n] = wave_sum(accf[r][n]);
+            else acci[r][n] = wave_sum(acci[r][n]);
+        }
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {

@@ -72,7 +72,7 @@ __global__ void __launch_bounds__(256) int8_rowsum(const int8_t* A, int M, int K
     if (row >= M) return;
     int s = 0;
     for (int k = lane; k < K; k += 64) s += A[(int64_t)row * K + k];
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    s = wave_sum(s);
     if (lane == 0) out[row] = s;
 }
 

@@ -202,12 +202,12 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
             }
         }
     }
+    // the wave's sums (a fixed butterfly, permlane swaps and DPP): every lane
+    // ends with the totals
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
+    for (int r = 0; r < RPW; ++r)
 #pragma unroll
-        for (int r = 0; r < RPW; ++r)
-#pragma unroll
-            for (int t = 0; t < TV; ++t) acc[r][t] += __shfl_xor(acc[r][t], off);
+        for (int t = 0; t < TV; ++t) acc[r][t] = wave_sum(acc[r][t]);
     // lane t (t < T) writes token t of every row
     if constexpr (SWIGLU) {
 #pragma unroll
