@@ -27,11 +27,13 @@
 //
 // RAWB (group-wise INT4 with 15 or 16 columns): no transpose pre-pass.  B
 // [K, 8] bytes (16 nibbles per k row) is contiguous, so each wave copies the
-// 1 KB of every group it owns into LDS by LDS DMA at the start, and in step q
-// a lane gathers the nibble of its column from the 8 rows of k = 32 q + 8 h
-// (two distinct dwords per 16-lane group: broadcast reads), packs them in the
-// weights' nibble order and unpacks them with the same exact (q - z) 2^-9
-// arithmetic; the extra 2^-9 is returned in the fold.
+// 1 KB of every group it owns into LDS by LDS DMA at the start and reorders
+// it there once, in place: an 8 x 8 nibble transpose (three stages of masked
+// swaps of 16-, 8- and 4-bit fields) turns the 8 rows k = 32 q + 8 h .. + 7 of
+// 8 columns into one dword per column in the weights' nibble order, stored
+// so that lane (h, column) finds the dwords of its four steps in one 16-byte
+// slot.  They are unpacked with the same exact (q - z) 2^-9 arithmetic; the
+// extra 2^-9 is returned in the fold.
 #pragma once
 
 #include "i4w_gemm.hpp"
@@ -65,6 +67,30 @@ __device__ __forceinline__ u32x4 transpose_lane_groups(u32x4 v) {
     return u32x4{c[0], d[0], c[1], d[1]};
 }
 
+// 8 x 8 transpose of 4-bit fields: nibble j of x[i] goes to nibble i of x[j]
+// (three stages of field swaps between registers 4, 2 and 1 apart)
+__device__ __forceinline__ void nibble_transpose8(unsigned (&x)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned a = x[i], b = x[i + 4];
+        x[i] = (a & 0x0000ffffu) | (b << 16);
+        x[i + 4] = (a >> 16) | (b & 0xffff0000u);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = (j & 1) + 4 * (j >> 1);  // 0, 1, 4, 5
+        const unsigned a = x[i], b = x[i + 2];
+        x[i] = (a & 0x00ff00ffu) | ((b << 8) & 0xff00ff00u);
+        x[i + 2] = ((a >> 8) & 0x00ff00ffu) | (b & 0xff00ff00u);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const unsigned a = x[i], b = x[i + 1];
+        x[i] = (a & 0x0f0f0f0fu) | ((b << 4) & 0xf0f0f0f0u);
+        x[i + 1] = ((a >> 4) & 0x0f0f0f0fu) | (b & 0xf0f0f0f0u);
+    }
+}
+
 template <class SC, bool XS, int OUT, bool RAWB = false>
 __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     constexpr int WF = SC::WF, XF = SC::XF, NG = SC::NG, D = SC::D, ROWS = SC::ROWS;
@@ -92,16 +118,18 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     for (int j = 0; j < XF; ++j)
         xrow[j] = RAWB ? nullptr : p.X + (int64_t)min(16 * j + l16, p.C - 1) * K + 8 * h;
 
+    // RAWB: this wave's groups of B (1 KB each: 128 k rows x 8 bytes), 16
+    // bytes a lane, loaded ahead of every other load.  Ordinary loads, not LDS
+    // DMA: loads complete in order, so the wait for these waits for nothing
+    // issued after them, where a read of LDS behind an LDS DMA waits for every
+    // outstanding load, the weight stream included.  (A wave without groups
+    // loads group G - 1 and stores none of it.)
+    u32x4 braw[RAWB ? NG : 1];
     if constexpr (RAWB) {
-        // this wave's groups of B (1 KB each: 128 k rows x 8 bytes) to LDS,
-        // ahead of every other load so that the first wait for those covers them
-        const u32x4 rb = dma::make_rsrc(p.B, (unsigned)K * 8);
-        const unsigned lb = __builtin_amdgcn_readfirstlane(
-            (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char*)lds_b));
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
             const int g = max(0, min(g0 + j, g1 - 1));
-            dma::dma16(rb, lb + (unsigned)g * 1024u, 16 * lane, g * 1024);
+            braw[j] = *reinterpret_cast<const u32x4*>(p.B + (int64_t)g * 1024 + 16 * lane);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -179,6 +207,46 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
 #pragma unroll
     for (int j = 0; j < D; ++j) issue(slot[j], j);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (RAWB) {
+        // this wave's groups of B to LDS, then from k-row order to step order.
+        // In group g, lane l's 16 bytes (rows 2 l, 2 l + 1) go to slot
+        // (l + g) % 64.  Unit u = (group, h, half d) reads dword d (columns
+        // 8 d .. 8 d + 7, column c at nibble c ^ 1) of the rows
+        // k = 32 q + 8 h + r, r < 8, q < 4, of its group and writes column
+        // col = 8 d + c's dword of step q to word q of slot 16 h + (col + g) % 16.
+        // The rotations by g spread the lanes of every access over the banks:
+        // two lanes a bank for the reads, the minimum four passes for the
+        // 16-byte writes, and the steps' reads stay one slot a lane.  Only the
+        // wave that owns a group touches it here, and one wave's LDS accesses
+        // take effect in program order: its copy lands before its reads, and
+        // its reads (each write needs all 32 of its lane's reads) before its
+        // writes.  The barrier below orders the reorder before the steps.
+#pragma unroll
+        for (int j = 0; j < NG; ++j)
+            if (g0 + j < g1)
+                *reinterpret_cast<u32x4*>(lds_b + (g0 + j) * 1024 + ((lane + g0 + j) & 63) * 16) = braw[j];
+        for (int u = lane; u < 8 * (g1 - g0); u += 64) {
+            const int g = g0 + (u >> 3), hh = (u >> 1) & 3, d = u & 1;
+            unsigned char* gb = lds_b + g * 1024;
+            unsigned y[4][8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                unsigned x[8];
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    x[r ^ 1] = *reinterpret_cast<const unsigned*>(
+                        gb + ((16 * q + 4 * hh + (r >> 1) + g) & 63) * 16 + 8 * (r & 1) + 4 * d);
+                nibble_transpose8(x);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) y[q][c] = x[c ^ 1];
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+                *reinterpret_cast<u32x4*>(gb + (16 * hh + ((8 * d + c + g) & 15)) * 16) =
+                    u32x4{y[0][c], y[1][c], y[2][c], y[3][c]};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
     stage_store(0);
     // (more than SPT elements per thread: rare, and those loads wait behind the stream)
     for (int base = SPT * SC::NT; base < nsz + nxs; base += SPT * SC::NT) {
@@ -210,28 +278,20 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
                 zz[f] = f16x2{nz, nz};
             }
             f16x2 zzb;
-            unsigned bshift = 0;
-            const unsigned char* brow = nullptr;
+            u32x4 bq;
             if constexpr (RAWB) {
                 const _Float16 nzb = (_Float16)(-rintf(h2f(lds_zb[g * 16 + l16])) * (1.0f / 512.0f));
                 zzb = f16x2{nzb, nzb};
-                // column l16: byte l16 / 2 of a row, the high nibble for even columns
-                bshift = 8 * ((l16 >> 1) & 3) + ((l16 & 1) ? 0 : 4);
-                brow = lds_b + (g * 128 + 8 * h) * 8 + 4 * (l16 >> 3);
+                // column l16, rows k = 128 g + 32 q + 8 h .. + 7 in word q, packed
+                // as the weights are (byte j: row 2j high, row 2j + 1 low), in
+                // slot 16 h + (l16 + g) % 16
+                bq = *reinterpret_cast<const u32x4*>(lds_b + g * 1024 + (16 * h + ((l16 + g) & 15)) * 16);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 f16x8 xq[XF];
                 if constexpr (RAWB) {
-                    // rows k = 128 g + 32 q + 8 h + r, r < 8, packed as the weights
-                    // are: byte j holds row 2j in the high nibble, 2j + 1 in the low
-                    unsigned wx = 0;
-#pragma unroll
-                    for (int r = 0; r < 8; ++r) {
-                        const unsigned d = *reinterpret_cast<const unsigned*>(brow + (32 * q + r) * 8);
-                        wx |= ((d >> bshift) & 15u) << (8 * (r >> 1) + ((r & 1) ? 0 : 4));
-                    }
-                    xq[0] = unpack8(wx, zzb);
+                    xq[0] = unpack8(q == 0 ? bq.x : q == 1 ? bq.y : q == 2 ? bq.z : bq.w, zzb);
                 } else {
 #pragma unroll
                     for (int x = 0; x < XF; ++x) xq[x] = s.x[x][q];
