@@ -13,9 +13,10 @@
 //    the row/column sums coming from a small pre-pass when a zero is non-zero.
 //    B [K,N] is N-contiguous: each thread transposes 4 K rows x 16 columns of
 //    bytes in registers (v_perm) on the way to LDS.
-//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads (a 256 x 256
-//    tile per workgroup, all in flight), int32 MADs on the VALU with the zero
-//    points subtracted directly, split-K over workgroups.
+//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads (a 128- or
+//    256-column tile per workgroup, all in flight), each column's four k rows
+//    of a thread transposed into one dword (v_perm) for one v_dot4_i32_i8,
+//    zero points by the same expansion, split-K over workgroups.
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "mfma_gemm.hpp"
@@ -362,30 +363,62 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
     }
     __builtin_amdgcn_sched_barrier(0);  // every B row requested before the first product
 
-    // Rows of A in passes of at most two (B stays in registers): the 16 column
-    // accumulators of four rows would not fit beside the loads in flight.
+    // Each column's four k rows (k = kbeg + kl + IV_KL j, j < 4) in one dword:
+    // a 4 x 4 byte transpose of the rows' 16-byte loads (v_perm), so that one
+    // v_dot4_i32_i8 forms a column's four products and their sum.  Zero points
+    // by  sum (a - za)(b - zb) = sum ab - za sum b - zb sum (a - za)  over the
+    // valid rows (int32, exact: every term is small).  Rows past K (loaded from
+    // the clamped last row) take a zero byte of A and of the row mask.
+    static_assert(IV_RPT == 4, "one dot4 per column covers a thread's four rows");
+    unsigned bc[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const unsigned lo01 = __builtin_amdgcn_perm(bv[1][c], bv[0][c], 0x05010400u);
+        const unsigned hi01 = __builtin_amdgcn_perm(bv[1][c], bv[0][c], 0x07030602u);
+        const unsigned lo23 = __builtin_amdgcn_perm(bv[3][c], bv[2][c], 0x05010400u);
+        const unsigned hi23 = __builtin_amdgcn_perm(bv[3][c], bv[2][c], 0x07030602u);
+        bc[4 * c] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);      // rows 0-3 of column 4c
+        bc[4 * c + 1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);  // column 4c + 1
+        bc[4 * c + 2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+        bc[4 * c + 3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    }
+    unsigned ok4 = 0;  // byte j: 1 when row j lies inside K
+    int nok = 0;
+#pragma unroll
+    for (int j = 0; j < IV_RPT; ++j)
+        if (kbeg + kl + IV_KL * j < K) {
+            ok4 |= 1u << (8 * j);
+            ++nok;
+        }
+
+    // Rows of A in passes of at most two: the 16 column accumulators of four
+    // rows would not fit beside the loads in flight.
     constexpr int MC = MM >= 4 ? 2 : MM;
 #pragma unroll
     for (int m0 = 0; m0 < MM; m0 += MC) {
         int acc[MC][16];
 #pragma unroll
-        for (int m = 0; m < MC; ++m)
+        for (int m = 0; m < MC; ++m) {
+            const bool in_m = m0 + m < M;
+            unsigned ap = 0;  // byte j: row j's A value (zero past K or past M)
+            int asum = 0;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[m][e] = 0;
+            for (int j = 0; j < IV_RPT; ++j) {
+                const int av = (in_m && kbeg + kl + IV_KL * j < K) ? (int)xa[m0 + m][j] : 0;
+                ap |= ((unsigned)av & 0xffu) << (8 * j);
+                asum += av;
+            }
 #pragma unroll
-        for (int j = 0; j < IV_RPT; ++j) {
-            const bool row_ok = kbeg + kl + IV_KL * j < K;
-            const unsigned w[4] = {bv[j].x, bv[j].y, bv[j].z, bv[j].w};
-            // |a - za|, |b - zb| <= 255: 24-bit products are exact
-            int a[MC];
+            for (int e = 0; e < 16; ++e) acc[m][e] = __builtin_amdgcn_sdot4((int)ap, (int)bc[e], 0, false);
+            if (p.za != 0) {
+                const int mk = in_m ? (int)ok4 : 0;
 #pragma unroll
-            for (int m = 0; m < MC; ++m) a[m] = (row_ok && m0 + m < M) ? (int)xa[m0 + m][j] - p.za : 0;
-            // each byte of B is extracted once and used for every row
+                for (int e = 0; e < 16; ++e) acc[m][e] -= p.za * __builtin_amdgcn_sdot4(mk, (int)bc[e], 0, false);
+            }
+            if (p.zb != 0) {
+                const int t = in_m ? asum - p.za * nok : 0;  // sum of (a - za) over the valid rows
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int b = __builtin_amdgcn_sbfe(w[e >> 2], (e & 3) * 8, 8) - p.zb;
-#pragma unroll
-                for (int m = 0; m < MC; ++m) acc[m][e] += __mul24(a[m], b);
+                for (int e = 0; e < 16; ++e) acc[m][e] -= p.zb * t;
             }
         }
         // the k lanes of a column lane: with 8 column lanes first lanes l and
