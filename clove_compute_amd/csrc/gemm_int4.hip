@@ -351,12 +351,12 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     return g;
 }
 
-template <int NV, int MODE, int RPW, int UPR>
-clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
+template <int NV, int MODE, int RPW, int UPR, bool ALIGNED>
+clove_status_t run_gemv_shape(const GemvParams& p, int wpb, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(NV, p.nch, p.G);
-    wpb = min(wpb, (aligned ? gemv_max_threads<NV, true, 4>() : gemv_max_threads<NV, false, 4>()) / 64);
+    wpb = min(wpb, gemv_max_threads<NV, ALIGNED, 4>() / 64);
     const dim3 grid(cdiv(p.M, wpb * RPW));
-    auto k = aligned ? int4_gemv<NV, MODE, RPW, UPR, true> : int4_gemv<NV, MODE, RPW, UPR, false>;
+    auto k = int4_gemv<NV, MODE, RPW, UPR, ALIGNED>;
     if (ensure_lds(reinterpret_cast<const void*>(k), (int)lds) != CLOVE_OK) return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
@@ -365,20 +365,24 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
 template <int NV, int MODE>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
     const GemvShape g = gemv_shape(p.M, p.nch, cus);
+    // unaligned rows are assembled from byte loads (16 registers per chunk
+    // until packed): one row per wave and one chunk per lane at a time, so
+    // that the variant needs no scratch
+    if (!aligned) return run_gemv_shape<NV, MODE, 1, 1, false>(p, g.wpb, stream);
     // (rpw, upr) pairs keep rpw * upr <= 8 chunk loads per lane
     if (g.rpw == 1) {
-        if (g.upr >= 8) return run_gemv_shape<NV, MODE, 1, 8>(p, g.wpb, aligned, stream);
-        if (g.upr >= 6) return run_gemv_shape<NV, MODE, 1, 6>(p, g.wpb, aligned, stream);
-        if (g.upr >= 4) return run_gemv_shape<NV, MODE, 1, 4>(p, g.wpb, aligned, stream);
-        if (g.upr >= 2) return run_gemv_shape<NV, MODE, 1, 2>(p, g.wpb, aligned, stream);
-        return run_gemv_shape<NV, MODE, 1, 1>(p, g.wpb, aligned, stream);
+        if (g.upr >= 8) return run_gemv_shape<NV, MODE, 1, 8, true>(p, g.wpb, stream);
+        if (g.upr >= 6) return run_gemv_shape<NV, MODE, 1, 6, true>(p, g.wpb, stream);
+        if (g.upr >= 4) return run_gemv_shape<NV, MODE, 1, 4, true>(p, g.wpb, stream);
+        if (g.upr >= 2) return run_gemv_shape<NV, MODE, 1, 2, true>(p, g.wpb, stream);
+        return run_gemv_shape<NV, MODE, 1, 1, true>(p, g.wpb, stream);
     }
-    if (g.rpw == 2) return g.upr >= 4   ? run_gemv_shape<NV, MODE, 2, 4>(p, g.wpb, aligned, stream)
-                           : g.upr >= 2 ? run_gemv_shape<NV, MODE, 2, 2>(p, g.wpb, aligned, stream)
-                                        : run_gemv_shape<NV, MODE, 2, 1>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return g.upr >= 2 ? run_gemv_shape<NV, MODE, 4, 2>(p, g.wpb, aligned, stream)
-                                      : run_gemv_shape<NV, MODE, 4, 1>(p, g.wpb, aligned, stream);
-    return run_gemv_shape<NV, MODE, 8, 1>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr >= 4   ? run_gemv_shape<NV, MODE, 2, 4, true>(p, g.wpb, stream)
+                           : g.upr >= 2 ? run_gemv_shape<NV, MODE, 2, 2, true>(p, g.wpb, stream)
+                                        : run_gemv_shape<NV, MODE, 2, 1, true>(p, g.wpb, stream);
+    if (g.rpw == 4) return g.upr >= 2 ? run_gemv_shape<NV, MODE, 4, 2, true>(p, g.wpb, stream)
+                                      : run_gemv_shape<NV, MODE, 4, 1, true>(p, g.wpb, stream);
+    return run_gemv_shape<NV, MODE, 8, 1, true>(p, g.wpb, stream);
 }
 
 template <int MODE>

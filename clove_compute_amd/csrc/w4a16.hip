@@ -277,12 +277,12 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     return g;
 }
 
-template <int TV, int RPW, int UPR, bool SWIGLU = false>
-clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStream_t stream) {
+template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false>
+clove_status_t run_gemv_shape(const GemvParams& p, int wpb, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(TV, p.nch);
-    wpb = min(wpb, (aligned ? w4_max_threads<TV, RPW, UPR, true>() : w4_max_threads<TV, RPW, UPR, false>()) / 64);
+    wpb = min(wpb, w4_max_threads<TV, RPW, UPR, ALIGNED>() / 64);
     const dim3 grid(cdiv(p.O, wpb * (SWIGLU ? RPW / 2 : RPW)));
-    auto k = aligned ? w4a16_gemv<TV, RPW, UPR, true, SWIGLU> : w4a16_gemv<TV, RPW, UPR, false, SWIGLU>;
+    auto k = w4a16_gemv<TV, RPW, UPR, ALIGNED, SWIGLU>;
     if (ensure_lds(reinterpret_cast<const void*>(k), (int)lds) != CLOVE_OK) return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
@@ -293,34 +293,41 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, bool aligned, hipStr
 template <int TV>
 clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
     const GemvShape g = gemv_shape(2 * p.O, p.nch, cus);
+    // unaligned rows are assembled from byte loads (16 registers per chunk
+    // until packed): one gate / up pair per wave and one chunk per lane at a
+    // time, so that the variant needs no scratch
+    if (!aligned) return run_gemv_shape<TV, 2, 1, false, true>(p, g.wpb, stream);
     // (a lane loads no more chunks per row than the row has: two-row waves
     // take 1, 2 or 4 chunk loads per row)
-    if (g.rpw == 1) return run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
-    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1, true>(p, g.wpb, aligned, stream)
-                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2, true>(p, g.wpb, aligned, stream)
-                                        : run_gemv_shape<TV, 2, 4, true>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1, true>(p, g.wpb, aligned, stream)
-                                      : run_gemv_shape<TV, 4, 2, true>(p, g.wpb, aligned, stream);
-    return run_gemv_shape<TV, 8, 1, true>(p, g.wpb, aligned, stream);
+    if (g.rpw == 1) return run_gemv_shape<TV, 2, 4, true, true>(p, g.wpb, stream);
+    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1, true, true>(p, g.wpb, stream)
+                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2, true, true>(p, g.wpb, stream)
+                                        : run_gemv_shape<TV, 2, 4, true, true>(p, g.wpb, stream);
+    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1, true, true>(p, g.wpb, stream)
+                                      : run_gemv_shape<TV, 4, 2, true, true>(p, g.wpb, stream);
+    return run_gemv_shape<TV, 8, 1, true, true>(p, g.wpb, stream);
 }
 
 template <int TV>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
     const GemvShape g = gemv_shape(p.O, p.nch, cus);
+    // (unaligned rows: one row per wave and one chunk per lane at a time, as
+    // for the SwiGLU variant)
+    if (!aligned) return run_gemv_shape<TV, 1, 1, false>(p, g.wpb, stream);
     // (rpw, upr) pairs keep rpw * upr <= 8 chunk loads per lane
     if (g.rpw == 1) {
-        if (g.upr >= 8) return run_gemv_shape<TV, 1, 8>(p, g.wpb, aligned, stream);
-        if (g.upr >= 6) return run_gemv_shape<TV, 1, 6>(p, g.wpb, aligned, stream);
-        if (g.upr >= 4) return run_gemv_shape<TV, 1, 4>(p, g.wpb, aligned, stream);
-        if (g.upr >= 2) return run_gemv_shape<TV, 1, 2>(p, g.wpb, aligned, stream);
-        return run_gemv_shape<TV, 1, 1>(p, g.wpb, aligned, stream);
+        if (g.upr >= 8) return run_gemv_shape<TV, 1, 8, true>(p, g.wpb, stream);
+        if (g.upr >= 6) return run_gemv_shape<TV, 1, 6, true>(p, g.wpb, stream);
+        if (g.upr >= 4) return run_gemv_shape<TV, 1, 4, true>(p, g.wpb, stream);
+        if (g.upr >= 2) return run_gemv_shape<TV, 1, 2, true>(p, g.wpb, stream);
+        return run_gemv_shape<TV, 1, 1, true>(p, g.wpb, stream);
     }
-    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1>(p, g.wpb, aligned, stream)
-                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2>(p, g.wpb, aligned, stream)
-                                        : run_gemv_shape<TV, 2, 4>(p, g.wpb, aligned, stream);
-    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1>(p, g.wpb, aligned, stream)
-                                      : run_gemv_shape<TV, 4, 2>(p, g.wpb, aligned, stream);
-    return run_gemv_shape<TV, 8, 1>(p, g.wpb, aligned, stream);
+    if (g.rpw == 2) return g.upr <= 1   ? run_gemv_shape<TV, 2, 1, true>(p, g.wpb, stream)
+                           : g.upr <= 2 ? run_gemv_shape<TV, 2, 2, true>(p, g.wpb, stream)
+                                        : run_gemv_shape<TV, 2, 4, true>(p, g.wpb, stream);
+    if (g.rpw == 4) return g.upr == 1 ? run_gemv_shape<TV, 4, 1, true>(p, g.wpb, stream)
+                                      : run_gemv_shape<TV, 4, 2, true>(p, g.wpb, stream);
+    return run_gemv_shape<TV, 8, 1, true>(p, g.wpb, stream);
 }
 
 using mg::Tile;

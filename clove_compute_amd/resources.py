@@ -8,12 +8,10 @@ spills registers to scratch memory; the HIP runtime then sizes and allocates
 that scratch on the kernel's first dispatch, outside any workspace a caller
 has bound.
 
-build() calls check(): it fails when a kernel spills that is not in
-ALLOWED_SPILLS (kernels only the unaligned fallback paths dispatch).
+build() calls check(): it fails when any kernel has a private segment.
 """
 from __future__ import annotations
 
-import fnmatch
 import glob
 import os
 import re
@@ -23,15 +21,6 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 OBJ = os.path.join(HERE, "_build")
 LLVM = "/opt/rocm/llvm/bin"
-
-# Mangled-name patterns of kernels allowed a private segment: the byte-gathering
-# unaligned GEMV variants (operands not 16-byte aligned or rows not a multiple
-# of the chunk size), which no aligned call reaches.  Every other kernel must
-# run without scratch.
-ALLOWED_SPILLS = [
-    "_ZN5clove2i49int4_gemvI*Lb0EEEvNS0_10GemvParamsE",        # int4_gemv<..., ALIGNED = false>
-    "_ZN5clove2w410w4a16_gemvI*Lb0ELb?EEEvNS0_10GemvParamsE",  # w4a16_gemv<..., ALIGNED = false, *>
-]
 
 _FIELDS = ("name", "private_segment_fixed_size", "vgpr_count", "agpr_count", "sgpr_count",
            "vgpr_spill_count", "sgpr_spill_count", "group_segment_fixed_size")
@@ -83,8 +72,7 @@ def report(objs: list[str] | None = None) -> list[dict]:
 
 
 def disallowed(rows: list[dict]) -> list[dict]:
-    return [r for r in rows if r["scratch"] > 0
-            and not any(fnmatch.fnmatchcase(r["name"], p) for p in ALLOWED_SPILLS)]
+    return [r for r in rows if r["scratch"] > 0]
 
 
 def check(objs: list[str] | None = None) -> list[dict]:

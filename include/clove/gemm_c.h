@@ -223,11 +223,8 @@ clove_status_t clove_w4a16_swiglu(const void* X, const uint8_t* W_q, const void*
  *  - a bound workspace, clove_workspace_bind(ptr, bytes): calls on this thread
  *    take their split-K partials, completion counters and intermediates from
  *    [ptr, ptr + bytes) and allocate nothing; a call that needs more returns
- *    CLOVE_ERR_WORKSPACE and launches nothing.  (One exception: the GEMV
- *    variants for operands that are not 16-byte aligned -- INT4 with N <= 8 and
- *    W4A16 with T <= 4 -- spill registers to private scratch, which the HIP
- *    runtime sizes on their first launch; every kernel an aligned call
- *    reaches uses none, which the library build checks.)  ptr must be 256-byte aligned
+ *    CLOVE_ERR_WORKSPACE and launches nothing.  (No kernel uses private
+ *    scratch either, which the library build checks.)  ptr must be 256-byte aligned
  *    and bytes >= CLOVE_WORKSPACE_MIN_BYTES; the first CLOVE_WORKSPACE_MIN_BYTES
  *    (the counters) must be zero before the first call, and every call leaves
  *    them zero.  Calls that may run at the same time on the device (other
