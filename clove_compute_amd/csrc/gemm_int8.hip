@@ -13,8 +13,8 @@
 //    the row/column sums coming from a small pre-pass when a zero is non-zero.
 //    B [K,N] is N-contiguous: each thread transposes 4 K rows x 16 columns of
 //    bytes in registers (v_perm) on the way to LDS.
-//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads (a 128- or
-//    256-column tile per workgroup, all in flight), each column's four k rows
+//  * int8_gemv -- M <= 4: B streamed once with 16-byte loads (a 256-column
+//    tile per workgroup, all in flight), each column's four k rows
 //    of a thread transposed into one dword (v_perm) for one v_dot4_i32_i8,
 //    zero points by the same expansion, split-K over workgroups.
 #include "common.hpp"
@@ -308,33 +308,24 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
 // GEMV (M <= 4): 1024 threads = CL column lanes x (1024 / CL) K lanes; a
 // column lane owns 16 consecutive columns (one 16-byte load per K row).
 // ---------------------------------------------------------------------------
-// A workgroup owns 16 CL columns x 512 k-rows of B (MM <= 2: 128 columns, 8
-// column lanes, 128 k lanes) or 256 columns x 256 k-rows (MM = 4: 16 column
-// lanes, 64 k lanes; 4 output rows of accumulators beside 8 rows of B in
-// flight would exceed the 128 VGPRs of a 1024-thread workgroup): thread
-// (kl, cl) loads the 16 bytes of columns 16cl..16cl+15 of rows kl + KL j,
-// j < 4, so each wave instruction reads whole 128- or 256-byte row segments
-// and the workgroup's 64 KB tile is requested at once (4096 x 4096, M = 1:
-// 256 workgroups; 7.9 us against 8.2 with 256 columns x 512 rows and 9.8 with
-// 256 x 256, measured with the partial-tile reduction; M = 4 at 128 columns
-// and two rows per thread took 21.7 us against 13.9).  Loads are
-// unconditional from clamped addresses (masked at use).  int32 sums: within a
-// wave (DPP and v_permlane row swaps), across the 16 waves through LDS, then
-// across the K splits (one round trip, see the end of the kernel).
-template <int MM>
-constexpr int iv_cols() { return MM >= 4 ? 256 : 128; }
-template <int MM>
-constexpr int iv_kl() { return 1024 / (iv_cols<MM>() / 16); }
-template <int MM>
-constexpr int iv_rpt() { return 4; }
-template <int MM>
-constexpr int iv_rows() { return iv_kl<MM>() * iv_rpt<MM>(); }
+// A workgroup owns 256 columns x 256 k-rows of B (16 column lanes, 64 k
+// lanes): thread (kl, cl) loads the 16 bytes of columns 16cl..16cl+15 of rows
+// kl + 64 j, j < 4, so each wave instruction reads whole 256-byte row segments
+// and the workgroup's 64 KB tile is requested at once (4096 x 4096: 256
+// workgroups).  Measured on 4096 x 4096 with the one-round-trip split-K below:
+// M = 1 at 128 / 256 / 512 columns 6.43 / 5.92 / 5.90 us, M = 2 at 128 / 256
+// columns 7.47 / 6.95 us.  Loads are unconditional from clamped addresses
+// (masked at use).  int32 sums: within a wave (v_permlane row swaps), across
+// the 16 waves through LDS, then across the K splits (one round trip, see the
+// end of the kernel).
+constexpr int kIvCols = 256, kIvKl = 1024 / (kIvCols / 16), kIvRpt = 4, kIvRows = kIvKl * kIvRpt;
 
 template <int MM, int OUT>
 __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
-    constexpr int IV_RPT = iv_rpt<MM>(), IV_ROWS = iv_rows<MM>();
-    constexpr int IV_COLS = iv_cols<MM>(), IV_KL = iv_kl<MM>(), CL = IV_COLS / 16;  // CL: column lanes
-    __shared__ int red[16][MM][IV_COLS];
+    constexpr int IV_RPT = kIvRpt, IV_ROWS = kIvRows;
+    constexpr int IV_COLS = kIvCols, IV_KL = kIvKl, CL = IV_COLS / 16;  // CL: column lanes
+    __shared__ __attribute__((aligned(16))) int red[16][MM][IV_COLS];
+    static_assert(CL == 16, "column lanes");
     __shared__ int s_last;
     const int tid = threadIdx.x;
     const int cl = tid % CL, kl = tid / CL, wave = tid >> 6, lane = tid & 63;
@@ -421,27 +412,17 @@ __global__ void __launch_bounds__(1024) int8_gemv(I8Params p, int col_blocks) {
                 for (int e = 0; e < 16; ++e) acc[m][e] -= p.zb * t;
             }
         }
-        // the k lanes of a column lane: with 8 column lanes first lanes l and
-        // l ^ 8 (a DPP rotation by 8 within each 16-lane row), then (l, l+16,
-        // l+32, l+48) by row swaps: lane l of row r ends with column
-        // 16 cl + 4 u + r, u < 4 (with 8 column lanes, lanes l and l ^ 8 hold
-        // the same sums and the one with bit 3 clear writes them)
-        if constexpr (CL == 8) {
-#pragma unroll
-            for (int m = 0; m < MC; ++m)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[m][e] += __builtin_amdgcn_mov_dpp(acc[m][e], 0x128, 0xf, 0xf, false);
-        }
+        // the k lanes of a column lane are lanes l, l+16, l+32, l+48: row
+        // swaps leave lane l of row r with column 16 cl + 4 u + r, u < 4
 #pragma unroll
         for (int m = 0; m < MC; ++m)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int v = rows_sum4(acc[m][4 * u], acc[m][4 * u + 1], acc[m][4 * u + 2], acc[m][4 * u + 3]);
-                if (CL == 16 || (lane & 8) == 0) red[wave][m0 + m][cl * 16 + 4 * u + (lane >> 4)] = v;
-            }
+            for (int u = 0; u < 4; ++u)
+                red[wave][m0 + m][cl * 16 + 4 * u + (lane >> 4)] =
+                    rows_sum4(acc[m][4 * u], acc[m][4 * u + 1], acc[m][4 * u + 2], acc[m][4 * u + 3]);
     }
     __syncthreads();
-    // threads 0..255 own one column each from here on; every thread still
+    // threads 0..IV_COLS-1 own one column each from here on; every thread still
     // takes part in the arrival barrier
     const bool active = tid < IV_COLS;
     const int col = active ? tid : 0;
@@ -529,8 +510,8 @@ namespace {
 template <int OUT>
 clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     const int mm = p.M == 1 ? 1 : (p.M == 2 ? 2 : 4);
-    const int rows = mm == 1 ? iv_rows<1>() : (mm == 2 ? iv_rows<2>() : iv_rows<4>());
-    const int IV_COLS = mm == 4 ? iv_cols<4>() : iv_cols<1>();
+    const int rows = kIvRows;
+    const int IV_COLS = kIvCols;
     const int col_blocks = cdiv(p.N, IV_COLS);
     p.nsplit = cdiv(p.K, rows);
     p.k_per_split = rows;
@@ -538,7 +519,7 @@ clove_status_t run_gemv(I8Params p, hipStream_t stream) {
     p.counters = nullptr;
     if (p.nsplit > 1) {
         // the one-round-trip reduction needs one zeroed 64-bit word per output
-        // (mm x 256 per column block) in the counter region; a bound workspace
+        // (mm x IV_COLS per column block) in the counter region; a bound workspace
         // whose counter region is smaller takes the partial-tile reduction
         Scratch s;
         clove_status_t st = CLOVE_ERR_WORKSPACE;
