@@ -264,9 +264,41 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     {
         // groups past g1 reload the last one (an L2 hit; a wave without groups
         // reloads group G - 1) and fold with scale 0: straight-line code, so
-        // every wait the compiler places is for one slot
-        auto compute = [&](const Slot& s, int j) {
+        // every wait the compiler places is for one slot.
+        //
+        // The group's LDS constants (weight zero points and scales, sx, and
+        // for raw B its zero points and the lane's 16-byte slot), read one
+        // group ahead: a group's unpack and MFMAs then never wait for an LDS
+        // round trip
+        struct Cst {
+            uint16_t z[WF], s[WF];
+            f32x4 sx[XS ? XF : 1];
+            uint16_t zb;
+            u32x4 bq;
+        };
+        auto load_cst = [&](int j) {
+            Cst c{};
             const int g = max(0, min(g0 + j, g1 - 1));
+#pragma unroll
+            for (int f = 0; f < WF; ++f) {
+                c.z[f] = lds_z[(16 * f + l16) * G + g];
+                c.s[f] = lds_s[(16 * f + l16) * G + g];
+            }
+            if constexpr (XS) {
+#pragma unroll
+                for (int x = 0; x < XF; ++x)
+                    c.sx[x] = *reinterpret_cast<const f32x4*>(lds_xs + g * 16 * XF + 16 * x + 4 * h);
+            }
+            if constexpr (RAWB) {
+                c.zb = lds_zb[g * 16 + l16];
+                // column l16, rows k = 128 g + 32 q + 8 h .. + 7 in word q, packed
+                // as the weights are (byte j: row 2j high, row 2j + 1 low), in
+                // slot 16 h + (l16 + g) % 16
+                c.bq = *reinterpret_cast<const u32x4*>(lds_b + g * 1024 + (16 * h + ((l16 + g) & 15)) * 16);
+            }
+            return c;
+        };
+        auto compute = [&](const Slot& s, const Cst& c, int j) {
             const bool valid = g0 + j < g1;
             f32x4 P[XF][WF];
             u32x4 wt[WF];
@@ -274,24 +306,19 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
 #pragma unroll
             for (int f = 0; f < WF; ++f) {
                 wt[f] = transpose_lane_groups(s.w[f]);
-                const _Float16 nz = (_Float16)(-rintf(h2f(lds_z[(16 * f + l16) * G + g])) * (1.0f / 512.0f));
+                const _Float16 nz = (_Float16)(-rintf(h2f(c.z[f])) * (1.0f / 512.0f));
                 zz[f] = f16x2{nz, nz};
             }
             f16x2 zzb;
-            u32x4 bq;
             if constexpr (RAWB) {
-                const _Float16 nzb = (_Float16)(-rintf(h2f(lds_zb[g * 16 + l16])) * (1.0f / 512.0f));
+                const _Float16 nzb = (_Float16)(-rintf(h2f(c.zb)) * (1.0f / 512.0f));
                 zzb = f16x2{nzb, nzb};
-                // column l16, rows k = 128 g + 32 q + 8 h .. + 7 in word q, packed
-                // as the weights are (byte j: row 2j high, row 2j + 1 low), in
-                // slot 16 h + (l16 + g) % 16
-                bq = *reinterpret_cast<const u32x4*>(lds_b + g * 1024 + (16 * h + ((l16 + g) & 15)) * 16);
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 f16x8 xq[XF];
                 if constexpr (RAWB) {
-                    xq[0] = unpack8(q == 0 ? bq.x : q == 1 ? bq.y : q == 2 ? bq.z : bq.w, zzb);
+                    xq[0] = unpack8(q == 0 ? c.bq.x : q == 1 ? c.bq.y : q == 2 ? c.bq.z : c.bq.w, zzb);
                 } else {
 #pragma unroll
                     for (int x = 0; x < XF; ++x) xq[x] = s.x[x][q];
@@ -309,14 +336,11 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
 #pragma unroll
             for (int f = 0; f < WF; ++f) {
                 // (q - z) 2^-9 back to q - z; 0 for the reloaded tail groups
-                const float wsc = valid ? h2f(lds_s[(16 * f + l16) * G + g]) * (RAWB ? 262144.0f : 512.0f) : 0.0f;
+                const float wsc = valid ? h2f(c.s[f]) * (RAWB ? 262144.0f : 512.0f) : 0.0f;
 #pragma unroll
                 for (int x = 0; x < XF; ++x) {
                     f32x4 sc = {wsc, wsc, wsc, wsc};
-                    if constexpr (XS) {
-                        const f32x4 sx = *reinterpret_cast<const f32x4*>(lds_xs + g * 16 * XF + 16 * x + 4 * h);
-                        sc = sc * sx;
-                    }
+                    if constexpr (XS) sc = sc * c.sx[x];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[x][f][e] = fmaf(sc[e], P[x][f][e], acc[x][f][e]);
                 }
@@ -325,13 +349,18 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
         // sched_barrier: keep the loads where they are written (the scheduler
         // would sink them toward their use to save registers, which shortens
         // the prefetch to nothing)
+        Cst cur = load_cst(0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NG; ++j) {
-            compute(slot[j % D], j);
+            // (past the last group: a harmless reread of the last group's constants)
+            const Cst nxt = load_cst(j + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(slot[j % D], cur, j);
             __builtin_amdgcn_sched_barrier(0);
             if (j + D < NG) issue(slot[j % D], j + D);
             __builtin_amdgcn_sched_barrier(0);
+            cur = nxt;
         }
     }
 
