@@ -138,6 +138,19 @@ clove_status_t run_stream(const Args& a, int cus, hipStream_t stream) {
     return CLOVE_ERR_INVALID_ARG;
 }
 
+// Every workgroup of the streaming kernel reads all of X (C rows x K fp16),
+// so its cost grows with C x K per CU, while the split-K MFMA kernel reads
+// each X tile once per 64 weight rows and is flat in C.  Measured (W4A16,
+// T = 5..32 on 8192x2048, 2048x8192, 4096x4096, 4096x11008, 11008x4096): the
+// stream is ahead below ~256 KB of X per CU, counting one copy per round of
+// workgroups on a CU, and the MFMA kernel from there (4096x11008 T = 32:
+// 26.3 against 16.4 us; 2048x8192 T = 16: 12.2 against 10.8 us).
+bool stream_ahead(const Args& a, int cus) {
+    const bool wf2 = cdiv(a.R, 32) >= cus && (a.C <= 16 || a.G <= 64);  // run_stream's weight fragments
+    const int64_t rounds = cdiv(cdiv(a.R, wf2 ? 32 : 16), cus);
+    return (int64_t)a.C * a.K * 2 * rounds < 256 * 1024;
+}
+
 }  // namespace
 
 bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status_t* status) {
@@ -155,7 +168,7 @@ bool try_i4w_w4a16(const W4A16Args& w, int cus, hipStream_t stream, clove_status
     a.G = w.K / 128;
     a.alpha = w.alpha;
     a.beta = w.beta;
-    if (w.T <= 32 && a.G <= kStreamMaxGroups) {
+    if (w.T <= 32 && a.G <= kStreamMaxGroups && stream_ahead(a, cus)) {
         *status = run_stream<false, 1>(a, cus, stream);
         return true;
     }
