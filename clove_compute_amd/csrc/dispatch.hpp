@@ -121,6 +121,17 @@ clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gat
 clove_status_t acquire_buffer(hipStream_t stream, int slot, size_t bytes, void** out);
 constexpr int kBufSwiglu = 1;  // gate / up intermediates of the unfused SwiGLU paths
 
+// FP16 with two to four rows of A: the skinny MFMA kernel rather than the
+// GEMV once the weight is large (cold, measured: 11008 x 4096 at M = 2 / 3 /
+// 4: 21.1 / 21.3 / 21.0 us against 26.5 / 32.2 / 31.8 on the GEMV; 4096 x 4096
+// at M = 3: 12.6 against 13.8; 2048 x 2048 at M = 3 and 4096 x 4096 at M = 2
+// stay on the GEMV: 9.6 against 12.6, 11.8 against 12.6).  gemm_fp16 and the
+// fused SwiGLU take the same decision per projection.
+inline bool skinny_before_gemv(int M, int N, int K) {
+    const int64_t nk = (int64_t)N * K;
+    return M >= 2 && M <= 4 && nk > (M == 2 ? ((int64_t)24 << 20) : ((int64_t)5 << 20));
+}
+
 // MFMA path for few rows of A against a large N-contiguous B (skinny_gemm.hip):
 // FP16 (any alpha/beta, batched) and INT8 with zero points 0.  Same contract
 // as the try_i4w_* functions.
@@ -128,7 +139,8 @@ bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batc
                      float alpha, float beta, int num_cus, hipStream_t stream, clove_status_t* status);
 bool try_skinny_int8(const Int8Args& args, int num_cus, hipStream_t stream, clove_status_t* status);
 // out [T, inter] = swiglu(fp16(X @ W_gate), fp16(X @ W_up)) in one pass of the
-// skinny kernel with two B operands (T > 4, aligned, hidden % 64 == 0); same
+// skinny kernel with two B operands (T > 4, or skinny_before_gemv; aligned,
+// hidden % 64 == 0); same
 // tiles and split plan as try_skinny_fp16 picks for each projection
 bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
                        int hidden, int inter, int num_cus, hipStream_t stream, clove_status_t* status);

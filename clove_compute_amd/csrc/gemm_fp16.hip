@@ -312,6 +312,10 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
                          (N % 8 == 0);
     const int64_t sA = (int64_t)M * K, sB = (int64_t)K * N, sC = (int64_t)M * N;
 
+    if (skinny_before_gemv(M, N, K)) {
+        clove_status_t st2;
+        if (try_skinny_fp16(A, B, C, batch, M, N, K, alpha, beta, dev.num_cus, stream, &st2)) return st2;
+    }
     if (aligned && M <= 4 && K > 0) {
         GemvParams g{A, B, C, nullptr, M, N, K, alpha, beta, sA, sB, sC, 0, 1, nullptr, nullptr};
         if (M == 1) return run_gemv<1>(g, batch, stream);

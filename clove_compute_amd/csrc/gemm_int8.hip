@@ -599,7 +599,7 @@ clove_status_t launch_gemm_int8(const Int8Args& a, hipStream_t stream) {
     p.scale = a.scale; p.za = a.za; p.zb = a.zb;
     p.M = a.M; p.N = a.N; p.K = a.K;
     const bool aligned = aligned16(a.A) && aligned16(a.B) && (a.K % 16 == 0) && (a.N % 16 == 0);
-    if (a.M > 4) {
+    if (a.M > 2) {  // (three or four rows only for large weights; try_skinny_int8 decides)
         clove_status_t st2;
         if (try_skinny_int8(a, dev.num_cus, stream, &st2)) return st2;
     }

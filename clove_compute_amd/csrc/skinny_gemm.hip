@@ -77,7 +77,8 @@ F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
 }
 
 bool f16_domain(const void* A, const void* B, const void* C, int M, int N, int K) {
-    if (M <= 4 || K <= 0 || K % 64 != 0 || N < 8 || N % 8 != 0) return false;
+    if (M <= 1 || K <= 0 || K % 64 != 0 || N < 8 || N % 8 != 0) return false;
+    if (M <= 4 && !skinny_before_gemv(M, N, K)) return false;
     if (!aligned16(A) || !aligned16(B) || !aligned16(C)) return false;
     // (the DMA offsets of the padded rows m < M + 128 must stay 32-bit)
     return fits31((int64_t)(M + 128) * K * 2) && fits31((int64_t)K * N * 2) && fits31((int64_t)M * N * 2);
@@ -141,7 +142,11 @@ bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t
 }
 
 bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_status_t* status) {
-    if (q.M <= 4 || q.M > 512 || q.K <= 0 || q.K % 128 != 0 || q.N < 16 || q.N % 16 != 0) return false;
+    if (q.M <= 2 || q.M > 512 || q.K <= 0 || q.K % 128 != 0 || q.N < 16 || q.N % 16 != 0) return false;
+    // three or four rows: the GEMV unless the weight is large (cold 11008 x 4096
+    // and 4096 x 11008, M = 3 / 4: 13.9 / 17.1 us here against 21.7 / 20.5 us
+    // on the GEMV; at 4096 x 4096 the GEMV is ahead, 9.2 against 11.5 us)
+    if (q.M <= 4 && (int64_t)q.N * q.K <= ((int64_t)32 << 20)) return false;
     if (q.za != 0 || q.zb != 0 || !aligned16(q.A) || !aligned16(q.B) || !aligned16(q.C)) return false;
     if (!fits31((int64_t)(q.M + 128) * q.K) || !fits31((int64_t)q.K * q.N) || !fits31((int64_t)q.M * q.N * 4))
         return false;

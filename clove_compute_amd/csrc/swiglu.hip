@@ -9,7 +9,8 @@
 //  * swiglu_fused on FP16 weights [hidden, intermediate] (the reference's
 //    gemm_fp16 B layout), one launch that writes neither projection to
 //    memory: the FP16 GEMV with two weight operands for T <= 4, the skinny
-//    MFMA kernel with two B operands for T > 4 (both bit-identical to two
+//    MFMA kernel with two B operands for T > 4 and for T = 2..4 on large
+//    weights, as gemm_fp16 decides per projection (both bit-identical to two
 //    gemm_fp16 calls followed by swiglu on the shapes where gemm_fp16 takes
 //    the same kernel family), and for shapes outside both (unaligned
 //    operands, hidden % 64 != 0 at T > 4) swiglu_fused_direct: one thread per
@@ -105,6 +106,11 @@ clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gat
     DeviceInfo dev;
     clove_status_t st = current_device_info(&dev);
     if (st != CLOVE_OK) return st;
+    // (the kernel family gemm_fp16 takes for each projection: the skinny
+    // kernel first where it would, then the GEMV for T <= 4)
+    if (skinny_before_gemv(T, inter, hidden) &&
+        try_skinny_swiglu(X, W_gate, W_up, out, T, hidden, inter, dev.num_cus, stream, &st))
+        return st;
     if (try_gemv_swiglu(X, W_gate, W_up, out, T, hidden, inter, stream, &st)) return st;
     if (try_skinny_swiglu(X, W_gate, W_up, out, T, hidden, inter, dev.num_cus, stream, &st)) return st;
     constexpr int TT = 4;

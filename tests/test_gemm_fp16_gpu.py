@@ -244,10 +244,12 @@ def test_skinny_shapes(M, N, K):
     check_rows(A, B, C, rows, C0, 0.75, -0.5)
 
 
-@pytest.mark.parametrize("M,N,K", [(7, 4096, 4096), (100, 264, 640), (128, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(7, 4096, 4096), (100, 264, 640), (128, 4096, 4096),
+                                   (3, 4096, 4096), (2, 11008, 4096), (4, 4096, 11008)])
 def test_skinny_small_integers_bit_exact(M, N, K):
     # |a|, |b| <= 4 integers: every product and partial sum is exact in fp32,
-    # so split K and the fp16 output are exact
+    # so split K and the fp16 output are exact (M = 2..4 on these weights
+    # take the skinny kernel rather than the GEMV)
     g = rng("skinny-int", M, N, K)
     A = g.integers(-4, 5, (M, K)).astype(np.float16)
     B = g.integers(-4, 5, (K, N)).astype(np.float16)

@@ -128,8 +128,11 @@ def test_skinny_bit_exact(M, N, K):
 # M = 2..4 on the GEMV with several K splits, non-zero zero points: per-tensor,
 # row/column scales and the raw accumulators, each bit for bit
 @pytest.mark.parametrize("M,N,K,za,zb", [(2, 4096, 4096, 3, -5), (3, 512, 2048, -7, 11), (4, 512, 2048, 9, -2),
-                                         (4, 4096, 4096, 0, 0)])
+                                         (4, 4096, 4096, 0, 0), (3, 11008, 4096, 0, 0), (4, 4096, 11008, 0, 0),
+                                         (4, 11008, 4096, 3, -5)])
 def test_gemv_multirow_split_k(M, N, K, za, zb):
+    # (3 and 4 rows on 11008-wide weights take the skinny kernel when the zero
+    # points are 0, the GEMV otherwise)
     g = rng("gemv8-mm", M, N, K, za, zb)
     A = g.integers(-128, 128, (M, K)).astype(np.int8)
     B = g.integers(-128, 128, (K, N)).astype(np.int8)
