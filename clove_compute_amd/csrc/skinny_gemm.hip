@@ -62,17 +62,28 @@ bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 enum class F16Tile { kM32, kM128, kT128, kT64 };
 
 F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
+    const bool short_k = K <= 16 * F16M128::BK;  // no split K (see run)
+    const bool long_k = K >= 4096;
+    // 128x128 tiles, split K when they are few: for M > 256 once they cover
+    // half the CUs or K is long, for 128 < M <= 256 on long K and N >= 4096
+    // (cold weights, against 64x64 tiles for M > 256 and 128x64 up to 256:
+    // 11008x4096 at M = 192 44.3 against 64.2 us, 4096x11008 at M = 384 64.1
+    // against 108.6 us, 4096x4096 at M = 384 30.6 against 43.7 us, 2048x8192
+    // at M = 512 35.2 against 47.4 us; K = 2048 and N = 2048 stay as they
+    // were: 2048x2048 at M = 384 14.0 with 64x64 against 19.0, 2048x8192 at
+    // M = 160 24.0 with 128x64 against 26.0; 64x64 for short K with few tiles:
+    // 1024^3 8 us against 13)
     if (M > 256) {
         const int64_t t128 = (int64_t)cdiv(M, 128) * cdiv(N, 128) * batch;
-        return t128 >= cus / 2 ? F16Tile::kT128 : F16Tile::kT64;
+        return (t128 >= cus / 2 || long_k) ? F16Tile::kT128 : F16Tile::kT64;
     }
+    if (M > 128 && long_k && N >= 4096) return F16Tile::kT128;
     // 32-row tiles up to M = 64 (cold 4096 x 4096 weights: M = 40 / 48 / 64 at
     // 13.6 / 14.1 / 14.5 us against 14.9 / 15.3 / 15.5 with 64-row tiles), and
     // for short K with few 128-row tiles, where they make 4x the workgroups
     // without a split (512^3: 6.1 us against 7.2, measured)
-    const bool short_k = K <= 16 * F16M128::BK &&
-                         (int64_t)cdiv(M, F16M128::BM) * cdiv(N, F16M128::BN) * batch < cus / 2;
-    if (M <= 64 || short_k) return F16Tile::kM32;
+    const bool few = (int64_t)cdiv(M, F16M128::BM) * cdiv(N, F16M128::BN) * batch < cus / 2;
+    if (M <= 64 || (short_k && few)) return F16Tile::kM32;
     return F16Tile::kM128;
 }
 
