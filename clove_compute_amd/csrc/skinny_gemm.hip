@@ -153,7 +153,7 @@ bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t
 }
 
 bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_status_t* status) {
-    if (q.M <= 2 || q.M > 512 || q.K <= 0 || q.K % 128 != 0 || q.N < 16 || q.N % 16 != 0) return false;
+    if (q.M <= 2 || q.M > 2048 || q.K <= 0 || q.K % 128 != 0 || q.N < 16 || q.N % 16 != 0) return false;
     // three or four rows: the GEMV unless the weight is large (cold 11008 x 4096
     // and 4096 x 11008, M = 3 / 4: 13.9 / 17.1 us here against 21.7 / 20.5 us
     // on the GEMV; at 4096 x 4096 the GEMV is ahead, 9.2 against 11.5 us)
@@ -173,12 +173,18 @@ bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_statu
     a.K = q.K;
     auto pick = [&](auto out_tag) -> clove_status_t {
         constexpr int OUT = decltype(out_tag)::value;
-        // 32-row tiles up to M = 128 (cold 4096 x 4096 weights: M = 64 / 128 at
-        // 10.8 / 13.8 us against 15.0 / 15.3 with 64- and 128-row tiles; from
-        // M = 160 the 128-row tiles are ahead), and for short K as for FP16
+        // 32-row tiles up to M = 64, and up to 128 unless the weight is large
+        // (cold: 4096 x 4096 at M = 64 / 128 10.8 / 13.8 us against 15.0 / 15.3
+        // with 64- and 128-row tiles, 8192 x 2048 at M = 128 12.0 against 14.7;
+        // 11008 x 4096 at M = 128 24.2 with 128-row tiles against 30.6), from
+        // M = 160 the 128-row tiles, and for short K as for FP16.  Up to
+        // M = 2048 this kernel is ahead of the register-staged MFMA GEMM
+        // (4096 x 4096 at M = 768 / 2048 43.4 / 79.4 us against 66.8 / 156.1,
+        // 11008 x 4096 at M = 768 95.3 against 209.2); at M = 4096 it is not.
         const bool short_k = q.K <= 16 * I8M128::BK &&
                              (int64_t)cdiv(q.M, I8M128::BM) * cdiv(q.N, I8M128::BN) < cus / 2;
-        if (q.M <= 128 || short_k) return run<I8M32, OUT>(a, 1, cus, stream);
+        const bool large_w = (int64_t)q.N * q.K > ((int64_t)32 << 20);
+        if (q.M <= 64 || (q.M <= 128 && !large_w) || short_k) return run<I8M32, OUT>(a, 1, cus, stream);
         return run<I8M128, OUT>(a, 1, cus, stream);
     };
     switch (q.out) {
