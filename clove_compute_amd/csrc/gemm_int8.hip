@@ -19,6 +19,7 @@
 //    zero points by the same expansion, split-K over workgroups.
 #include "common.hpp"
 #include "dispatch.hpp"
+#include "i8_dma_gemm.hpp"
 #include "mfma_gemm.hpp"
 
 namespace clove {
@@ -576,6 +577,36 @@ clove_status_t run_mfma(I8Params p, int cus, hipStream_t stream) {
     return check_launch();
 }
 
+// the 256x256 LDS-DMA kernel (i8_dma_gemm.hpp): zero points 0, K % 128 == 0,
+// N % 16 == 0, 16-byte aligned operands under 2^31 bytes
+bool i8big_eligible(const I8Params& p) {
+    return p.za == 0 && p.zb == 0 && p.K > 0 && p.K % i8big::Cfg::BKB == 0 && p.N >= 16 && p.N % 16 == 0 &&
+           aligned16(p.A) && aligned16(p.B) && aligned16(p.C) && (int64_t)p.M * p.K < (1ll << 31) &&
+           (int64_t)p.K * p.N < (1ll << 31) && (int64_t)p.M * p.N * 4 < (1ll << 31);
+}
+
+template <int OUT>
+clove_status_t run_i8big(const I8Params& q, hipStream_t stream) {
+    i8big::Args a{};
+    a.A = q.A;
+    a.B = q.B;
+    a.C = q.C;
+    a.sa = q.sa;
+    a.sb = q.sb;
+    a.scale = q.scale;
+    a.M = q.M;
+    a.N = q.N;
+    a.K = q.K;
+    a.tiles_m = cdiv(q.M, i8big::Cfg::BM);
+    a.tiles_n = cdiv(q.N, i8big::Cfg::BN);
+    constexpr int KO = OUT == (int)Int8Out::kAcc32       ? (int)i8big::kAcc32
+                       : OUT == (int)Int8Out::kHalfRowCol ? (int)i8big::kRowCol
+                                                          : (int)i8big::kTensor;
+    CLOVE_LAUNCH((i8big::gemm_i8_big<KO>), dim3((unsigned)(a.tiles_m * a.tiles_n)), dim3(i8big::Cfg::NT), 0,
+                 stream, a);
+    return check_launch();
+}
+
 template <int OUT>
 clove_status_t dispatch(I8Params p, bool aligned, int cus, hipStream_t stream) {
     if (aligned && p.M <= 4 && p.K > 0 && p.N >= 16) return run_gemv<OUT>(p, stream);
@@ -599,6 +630,17 @@ clove_status_t launch_gemm_int8(const Int8Args& a, hipStream_t stream) {
     p.scale = a.scale; p.za = a.za; p.zb = a.zb;
     p.M = a.M; p.N = a.N; p.K = a.K;
     const bool aligned = aligned16(a.A) && aligned16(a.B) && (a.K % 16 == 0) && (a.N % 16 == 0);
+    // 256x256 tiles once they cover half the CUs (cold weights, against the
+    // skinny kernel: 4096^3 146.5 -> 64.1 us, 11008x4096 at M = 768 94.2 ->
+    // 50.2 us, 8192x8192 at M = 1024 153.3 -> 86.1 us; with fewer tiles the
+    // skinny kernel is ahead: 4096x4096 at M = 1024 43.9 against 60.1 us)
+    if ((int64_t)cdiv(a.M, i8big::Cfg::BM) * cdiv(a.N, i8big::Cfg::BN) >= dev.num_cus / 2 && i8big_eligible(p)) {
+        switch (a.out) {
+            case Int8Out::kHalfPerTensor: return run_i8big<(int)Int8Out::kHalfPerTensor>(p, stream);
+            case Int8Out::kHalfRowCol: return run_i8big<(int)Int8Out::kHalfRowCol>(p, stream);
+            case Int8Out::kAcc32: return run_i8big<(int)Int8Out::kAcc32>(p, stream);
+        }
+    }
     if (a.M > 2) {  // (three or four rows only for large weights; try_skinny_int8 decides)
         clove_status_t st2;
         if (try_skinny_int8(a, dev.num_cus, stream, &st2)) return st2;

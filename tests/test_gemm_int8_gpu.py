@@ -148,3 +148,31 @@ def test_gemv_multirow_split_k(M, N, K, za, zb):
     assert np.array_equal(run_acc32(A, B, za, zb), accref)
     assert np.array_equal(f16bits(to_host(C1)), f16bits(Cref1))
     assert np.array_equal(f16bits(to_host(C2)), f16bits(Cref2))
+
+
+# 256x256 tiles covering half the CUs: the LDS-DMA kernel (i8_dma_gemm.hpp);
+# ragged M and N edges, K / 128 odd and 2; per-tensor, row / column scales
+# and the raw accumulators, bit for bit on sampled rows
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4100, 2000, 256), (2304, 3968, 640), (768, 11008, 512)])
+def test_big_tile(M, N, K):
+    import torch
+    g = rng("i8big", M, N, K)
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    sa = g.uniform(0.001, 0.02, M).astype(np.float16)
+    sb = g.uniform(0.001, 0.02, N).astype(np.float16)
+    s1, s2 = np.float32(g.uniform(0.001, 0.05)), np.float32(g.uniform(0.001, 0.05))
+    dA, dB = to_dev(A), to_dev(B)
+    C1, C2 = empty_f16(M, N), empty_f16(M, N)
+    acc = torch.empty(M, N, dtype=torch.int32, device="cuda")
+    cg = _cg()
+    cg.gemm_int8(dA, dB, C1, M, N, K, float(s1), 0, float(s2), 0)
+    cg.gemm_int8_rowcol(dA, dB, to_dev(sa), to_dev(sb), C2, M, N, K)
+    cg.gemm_int8_acc32(dA, dB, acc, M, N, K, 0, 0)
+    _sync()
+    rows = np.unique(np.concatenate([[0, 255, 256, M - 1], g.integers(0, M, 24)]))
+    Cref1, accref = oracle.gemm_int8(A[rows], B, s1, 0, s2, 0)
+    Cref2, _ = oracle.gemm_int8_rowcol(A[rows], B, sa[rows], sb)
+    assert np.array_equal(acc.cpu().numpy()[rows], accref)
+    assert np.array_equal(f16bits(to_host(C1)[rows]), f16bits(Cref1))
+    assert np.array_equal(f16bits(to_host(C2)[rows]), f16bits(Cref2))
