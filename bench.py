@@ -338,8 +338,9 @@ def extras():
                PEAK_FP16_TFLOPS)
         del Bs, Cs, calls
 
-    # ---- INT8 W8A8 with per-row / per-column fp16 scales ----
-    for M in (1, 128):
+    # ---- INT8 W8A8 with per-row / per-column fp16 scales: the decode / small
+    # batch rows of config 3 (weights cold), and the prefill square 4096^3 ----
+    for M in (1, 128, 4096):
         N = K = 4096
         a8 = i8((M, K), 8 + M)
         sa = uni16((M,), 0.001, 0.02, 9)
