@@ -221,6 +221,66 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
             }
         }
         lds_barrier();
+    } else if (NV > 2 && p.ldb <= 4 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0) {
+        // 3 to 8 columns (1 to 4 bytes per k row): word w of every column from
+        // rows 8w .. 8w + 7, one vector load for 1, 2 or 4 bytes per row, byte
+        // loads for 3 bytes and for the rows of the last word (rows past K
+        // read as zero)
+        const int ldb = p.ldb;
+        for (int w = tid; w < KW; w += NT) {
+            const int k0 = 8 * w;
+            unsigned rowb[8];  // row j's bytes, byte b of the row at bits 8b
+            if (k0 + 8 <= K && ldb != 3) {
+                if (ldb == 4) {
+                    const u32x4 v0 = *reinterpret_cast<const u32x4*>(p.B + 4 * k0);
+                    const u32x4 v1 = *reinterpret_cast<const u32x4*>(p.B + 4 * k0 + 16);
+                    rowb[0] = v0.x; rowb[1] = v0.y; rowb[2] = v0.z; rowb[3] = v0.w;
+                    rowb[4] = v1.x; rowb[5] = v1.y; rowb[6] = v1.z; rowb[7] = v1.w;
+                } else if (ldb == 2) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(p.B + 2 * k0);
+                    const unsigned d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) rowb[j] = (d[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                } else {
+                    const u32x2 v = *reinterpret_cast<const u32x2*>(p.B + k0);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) rowb[j] = ((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    unsigned r = 0;
+                    if (k0 + j < K)
+                        for (int b = 0; b < ldb; ++b) r |= (unsigned)p.B[(int64_t)(k0 + j) * ldb + b] << (8 * b);
+                    rowb[j] = r;
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < NV; ++n) {
+                // column n: byte n / 2 of a row, the high nibble for even n;
+                // packed in A's order (byte j: row 2j high, row 2j + 1 low)
+                unsigned word = 0;
+                if (n < p.cols_valid) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const unsigned nib = (rowb[j] >> (8 * (n >> 1) + ((n & 1) ? 0 : 4))) & 15u;
+                        word |= nib << (8 * (j >> 1) + ((j & 1) ? 0 : 4));
+                    }
+                }
+                Bw[n * KW + w] = word;
+            }
+        }
+        lds_barrier();
+        for (int idx = tid; idx < NV * nch; idx += NT) {
+            const int n = idx / nch, c = idx - n * nch;
+            const u32x4 bw = *reinterpret_cast<const u32x4*>(Bw + n * KW + 4 * c);
+            unsigned sb = __builtin_amdgcn_udot8(bw.x, kOnes, 0u, false);
+            sb = __builtin_amdgcn_udot8(bw.y, kOnes, sb, false);
+            sb = __builtin_amdgcn_udot8(bw.z, kOnes, sb, false);
+            sb = __builtin_amdgcn_udot8(bw.w, kOnes, sb, false);
+            Bc[idx] = chunk_consts(n, c, sb);
+        }
+        lds_barrier();
     } else {
         for (int idx = tid; idx < NV * KW; idx += NT) Bw[idx] = b_word(p, idx / KW, idx % KW);
         lds_barrier();

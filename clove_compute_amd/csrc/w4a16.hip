@@ -85,9 +85,12 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
     for (int r = 0; r < RPW; ++r)
         ridx[r] = (SWIGLU && r >= LR) ? p.O + min(row0 + r - LR, p.O - 1) : min(row0 + r % LR, p.O - 1);
 
-    // ---- X: 16-byte pieces (8 k) into registers first ----
+    // ---- X: 16-byte pieces (8 k) into registers first (the first XPT per
+    // thread; with several tokens, any further pieces are loaded at the
+    // staging -- one token always fits for K <= 32768) ----
     const int npieces = TV * KP / 8;
-    const bool xfast = npieces <= XPT * NT && (K & 7) == 0 && (reinterpret_cast<uintptr_t>(p.X) & 15) == 0;
+    const bool xfast = (TV > 1 || npieces <= XPT * NT) && (K & 7) == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.X) & 15) == 0;
     u32x4 xr[XPT];
     if (xfast) {
 #pragma unroll
@@ -147,6 +150,18 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
             const u32x4 o = {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
                              __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
             *reinterpret_cast<u32x4*>(Xs + t * KP + k8) = o;
+        }
+        // (more pieces than the prefetch holds: several tokens of a long row;
+        // loaded and stored the same way)
+        if constexpr (TV > 1) {
+            for (int q = tid + XPT * NT; q < npieces; q += NT) {
+                const int t = q / (KP / 8), k8 = (q - t * (KP / 8)) * 8;
+                u32x4 v = *reinterpret_cast<const u32x4*>(p.X + (int64_t)min(t, p.T - 1) * K + min(k8, K - 8));
+                if (t >= p.T || k8 >= K) v = u32x4{0u, 0u, 0u, 0u};
+                const u32x4 o = {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                                 __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+                *reinterpret_cast<u32x4*>(Xs + t * KP + k8) = o;
+            }
         }
     } else {
         for (int idx = tid; idx < TV * KP; idx += NT) {

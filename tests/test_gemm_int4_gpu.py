@@ -70,7 +70,7 @@ def test_config4_groupwise(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 1, 4096), (260, 8, 2048), (100, 16, 1024), (130, 128, 512),
-                                   (64, 3, 640)])
+                                   (64, 3, 640), (1024, 4, 11008), (512, 8, 4096), (96, 6, 4104)])
 def test_groupwise_pow2_bit_exact(M, N, K):
     # power-of-two scales, values q-z in [-1, 1]: every fp32/fp16 step is exact
     A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2", pow2=True, small=True)

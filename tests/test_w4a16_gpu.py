@@ -61,8 +61,9 @@ def test_llama1b_layer(T, name, O, K, beta):
 
 
 @pytest.mark.parametrize("T,O,K", [(1, 1024, 2048), (3, 520, 1024), (4, 256, 8192), (64, 512, 1024),
-                                   (300, 136, 256)])
+                                   (300, 136, 256), (4, 300, 11008), (2, 520, 16384)])
 def test_pow2_bit_exact(T, O, K):
+    # (T = 2..4 on long rows: more X pieces than the GEMV's prefetch holds)
     X, W, s, z, _ = make(T, O, K, "pow2", pow2=True)
     Y = run(X, W, s, z, None, O)
     _, ref = oracle.w4a16(X, W, s, z)
