@@ -6,8 +6,8 @@
 // (src/runtime/inference.cu:139-194, beta = 1 residual at :165-168, :191-194)
 // on INT4 weights.
 //
-//  * w4a16_gemv (T <= 4, decode) -- a wave streams one or more weight rows
-//    with 16-byte loads, all in flight at once; the nibbles are turned into the
+//  * w4a16_gemv (T <= 2, and T = 3, 4 on small weights: decode) -- a wave
+//    streams one or more weight rows with 16-byte loads, all in flight at once; the nibbles are turned into the
 //    exact fp16 integers q - z and dotted with X (staged in LDS) by
 //    v_dot2_f32_f16 in fp32; acc += scale * that per 32-k chunk.
 //  * larger T -- the INT4-weight MFMA GEMM (i4w_gemm.hpp) when K % 128 == 0
@@ -415,6 +415,11 @@ clove_status_t launch_w4a16(const W4A16Args& a, hipStream_t stream) {
     const int G = cdiv(a.K, 128);
     const int nch = cdiv(a.K, 32);
     const int tv = a.T <= 1 ? 1 : (a.T <= 2 ? 2 : 4);
+    if (a.K > 0 && a.T >= 3 && a.T <= 4) {
+        // (large weights: the streaming kernel, see try_i4w_w4a16)
+        clove_status_t st2;
+        if (try_i4w_w4a16(a, dev.num_cus, stream, &st2)) return st2;
+    }
     if (a.K > 0 && a.T <= 4 && gemv_lds_bytes(tv, nch) <= kMaxGemvLds) {
         GemvParams p{a.X, a.W, a.scale, a.zero, a.Y, a.T, a.O, a.K, G, nch, a.alpha, a.beta};
         const bool aligned = aligned16(a.W) && (a.K % 32 == 0);

@@ -109,8 +109,10 @@ def test_mfma_path_pow2_bit_exact(T, O, K):
 # and two 16-token fragments, one and two 16-row weight fragments per
 # workgroup (8192 rows), ragged weight rows, alpha/beta
 @pytest.mark.parametrize("T,O,K", [(5, 77, 128), (16, 300, 1280), (17, 130, 2560), (32, 1000, 3840),
-                                   (8, 8192, 5120), (31, 8192, 7680), (12, 4096, 11008 // 128 * 128)])
+                                   (8, 8192, 5120), (31, 8192, 7680), (12, 4096, 11008 // 128 * 128),
+                                   (3, 4096, 4096), (4, 1024, 11008 // 128 * 128)])
 def test_stream_path_shapes(T, O, K):
+    # (T = 3, 4 on weights above 8 Mi elements take the streaming kernel too)
     X, W, s, z, g = make(T, O, K, "stream")
     Yin = g.standard_normal((T, O)).astype(np.float16)
     Y = run(X, W, s, z, Yin, O, 0.75, 0.5)
