@@ -383,11 +383,13 @@ namespace {
 constexpr size_t kMaxGemvLds = 150 * 1024;
 
 // Rows per wave RPW and waves per workgroup: as many chunk loads per lane in
-// flight as fit (8), then enough workgroups to cover every CU.  Rows of 2 x 64
-// chunks (K 2049..4096) take small workgroups (8 waves of 2 rows): the rows
-// then spread over the CUs to within 1.1x of even, where 32-row workgroups
-// left some CUs twice the rows of others (11008 x 4096: 6.98 us against 7.66,
-// measured).
+// flight as fit (8), then workgroups halved until there are two per CU.  Rows
+// of 2 x 64 chunks (K 2049..4096) take small workgroups (8 waves of 2 rows):
+// the rows then spread over the CUs to within 1.1x of even, where 32-row
+// workgroups left some CUs twice the rows of others (11008 x 4096: 6.98 us
+// against 7.66, measured).  Two workgroups per CU rather than one (cold,
+// N = 1): 4096 x 11008 6.67 -> 6.32 us, 4096 x 14336 7.56 -> 7.21, 4096 x 4096
+// 4.07 -> 3.88; seven other weight shapes unchanged.
 struct GemvShape {
     int rpw, upr, wpb;
 };
@@ -399,7 +401,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl >= 3) g = {2, 4, 16};
     else if (cpl == 2) g = {2, 2, 8};
     else g = {8, 1, 16};
-    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
+    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < 2 * cus) g.wpb >>= 1;
     // one chunk per lane per row (K <= 2048): up to two workgroups per CU and
     // one chunk load per row, as for the W4A16 GEMV (w4a16.hip)
     const int target = cpl == 1 ? 2 * cus : cus;

@@ -271,7 +271,8 @@ constexpr size_t kMaxGemvLds = 150 * 1024;
 struct GemvShape {
     int rpw, upr, wpb;
 };
-inline GemvShape gemv_shape(int rows, int nch, int cus) {
+// (wg_min: workgroups per CU the first halving aims for)
+inline GemvShape gemv_shape(int rows, int nch, int cus, int wg_min = 1) {
     const int cpl = cdiv(nch, 64);
     GemvShape g{1, 8, 16};
     if (cpl >= 7) g = {1, 8, 16};
@@ -279,7 +280,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl >= 3) g = {2, 4, 16};
     else if (cpl == 2) g = {4, 2, 16};
     else g = {8, 1, 16};
-    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < cus) g.wpb >>= 1;
+    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < wg_min * cus) g.wpb >>= 1;
     // fewer rows per wave, up to two workgroups per CU: the rows spread over
     // the CUs evenly (3072 rows at K = 2048: 768 workgroups, 3 per CU, rather
     // than 384, some CUs holding twice the rows of others); a lane never
@@ -304,10 +305,14 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, hipStream_t stream) 
 }
 
 // SwiGLU: gate / up pairs, so at least two weight rows per wave (the shape
-// is chosen for the 2 O weight rows)
+// is chosen for the 2 O weight rows).  One token on rows of two or more chunks
+// per lane: workgroups halved to two per CU (cold: 11008 x 4096 16.0 -> 14.7
+// us, 14336 x 4096 19.7 -> 17.7, 4096 x 8192 11.9 -> 10.3; 2..4 tokens, whose
+// lanes hold more registers, and the plain GEMV measured slower or no better
+// with it: 14336 x 4096 T = 4 28.0 -> 36.1)
 template <int TV>
 clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
-    const GemvShape g = gemv_shape(2 * p.O, p.nch, cus);
+    const GemvShape g = gemv_shape(2 * p.O, p.nch, cus, TV == 1 && cdiv(p.nch, 64) >= 2 ? 2 : 1);
     // unaligned rows are assembled from byte loads (16 registers per chunk
     // until packed): one gate / up pair per wave and one chunk per lane at a
     // time, so that the variant needs no scratch

@@ -131,7 +131,7 @@ def check_rows(X, Wq, s, z, H, rows):
 # MLP (I = 8192, K = 2048) at decode and prefill
 @pytest.mark.parametrize("T,I,K", [(1, 8192, 2048), (2, 300, 1024), (3, 64, 256), (4, 1000, 4096),
                                    (5, 8192, 2048), (17, 200, 512), (33, 1000, 1024), (64, 96, 2048),
-                                   (100, 777, 384), (512, 8192, 2048)])
+                                   (100, 777, 384), (512, 8192, 2048), (1, 2000, 4096), (1, 1100, 8192)])
 def test_w4a16_swiglu_shapes(T, I, K):
     X, Wq, s, z, g = make_gate_up(T, I, K, "shapes")
     H = run_w4a16_swiglu(X, Wq, s, z, I)
