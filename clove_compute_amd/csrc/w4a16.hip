@@ -330,7 +330,15 @@ clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipSt
 
 template <int TV>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
-    const GemvShape g = gemv_shape(p.O, p.nch, cus);
+    GemvShape g = gemv_shape(p.O, p.nch, cus);
+    // one token on rows of two or more chunks per lane: workgroups halved until
+    // there are four per CU (rows of two chunks) or two (longer rows); cold:
+    // 14336 x 4096 9.9 -> 9.1 us, 4096 x 14336 10.8 -> 10.4, 4096 x 11008 9.35 ->
+    // 9.03, 11008 x 4096 8.0 -> 7.8, eight other weight shapes unchanged
+    if (TV == 1 && cdiv(p.nch, 64) >= 2) {
+        const int target = (cdiv(p.nch, 64) == 2 ? 4 : 2) * cus;
+        while (g.wpb > 4 && cdiv(p.O, g.wpb * g.rpw) < target) g.wpb >>= 1;
+    }
     // (unaligned rows: one row per wave and one chunk per lane at a time, as
     // for the SwiGLU variant)
     if (!aligned) return run_gemv_shape<TV, 1, 1, false>(p, g.wpb, stream);
