@@ -387,13 +387,15 @@ constexpr size_t kMaxGemvLds = 150 * 1024;
 // of 2 x 64 chunks (K 2049..4096) take small workgroups (8 waves of 2 rows):
 // the rows then spread over the CUs to within 1.1x of even, where 32-row
 // workgroups left some CUs twice the rows of others (11008 x 4096: 6.98 us
-// against 7.66, measured).  Two workgroups per CU rather than one (cold,
-// N = 1): 4096 x 11008 6.67 -> 6.32 us, 4096 x 14336 7.56 -> 7.21, 4096 x 4096
-// 4.07 -> 3.88; seven other weight shapes unchanged.
+// against 7.66, measured).  One or two columns: two workgroups per CU rather
+// than one (cold, N = 1: 4096 x 11008 6.67 -> 6.32 us, 4096 x 14336 7.56 ->
+// 7.21, 4096 x 4096 4.07 -> 3.88; N = 2: 4096 x 11008 7.46 -> 6.88; seven other
+// weight shapes unchanged); with four or eight columns, whose lanes hold more
+// registers, one (4096 x 4096 N = 4 6.0 against 6.4 us).
 struct GemvShape {
     int rpw, upr, wpb;
 };
-inline GemvShape gemv_shape(int rows, int nch, int cus) {
+inline GemvShape gemv_shape(int rows, int nch, int cus, int wg_min) {
     const int cpl = cdiv(nch, 64);
     GemvShape g{1, 8, 16};
     if (cpl >= 7) g = {1, 8, 16};
@@ -401,7 +403,7 @@ inline GemvShape gemv_shape(int rows, int nch, int cus) {
     else if (cpl >= 3) g = {2, 4, 16};
     else if (cpl == 2) g = {2, 2, 8};
     else g = {8, 1, 16};
-    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < 2 * cus) g.wpb >>= 1;
+    while (g.wpb > 4 && cdiv(rows, g.wpb * g.rpw) < wg_min * cus) g.wpb >>= 1;
     // one chunk per lane per row (K <= 2048): up to two workgroups per CU and
     // one chunk load per row, as for the W4A16 GEMV (w4a16.hip)
     const int target = cpl == 1 ? 2 * cus : cus;
@@ -426,7 +428,7 @@ clove_status_t run_gemv_shape(const GemvParams& p, int wpb, hipStream_t stream) 
 
 template <int NV, int MODE>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
-    const GemvShape g = gemv_shape(p.M, p.nch, cus);
+    const GemvShape g = gemv_shape(p.M, p.nch, cus, NV <= 2 ? 2 : 1);
     // unaligned rows are assembled from byte loads (16 registers per chunk
     // until packed): one row per wave and one chunk per lane at a time, so
     // that the variant needs no scratch
