@@ -339,6 +339,15 @@ clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t 
         const int target = (cdiv(p.nch, 64) == 2 ? 4 : 2) * cus;
         while (g.wpb > 4 && cdiv(p.O, g.wpb * g.rpw) < target) g.wpb >>= 1;
     }
+    // two to four tokens on rows of two or more chunks per lane: every
+    // workgroup stages all of X in LDS, so workgroups grow (while at least one
+    // per CU remains) until they hold 4 TV rows and the X copies stay within the
+    // weight bytes (cold: 2048 x 8192 T = 2 6.9 -> 6.1 us, 2048 x 4096 T = 4
+    // 6.2 -> 5.6; one-chunk rows and thinner grids measured slower with it)
+    if (TV > 1 && cdiv(p.nch, 64) >= 2) {
+        const int maxw = w4_max_threads<TV, 1, 1, true>() / 64;
+        while (g.wpb * g.rpw < 4 * TV && g.wpb * 2 <= maxw && cdiv(p.O, 2 * g.wpb * g.rpw) >= cus) g.wpb <<= 1;
+    }
     // (unaligned rows: one row per wave and one chunk per lane at a time, as
     // for the SwiGLU variant)
     if (!aligned) return run_gemv_shape<TV, 1, 1, false>(p, g.wpb, stream);

@@ -60,7 +60,8 @@ def test_llama1b_layer(T, name, O, K, beta):
     assert ok, (name, rep)
 
 
-@pytest.mark.parametrize("T,O,K", [(1, 1024, 2048), (1, 3000, 4096), (1, 2048, 11008), (3, 520, 1024),
+@pytest.mark.parametrize("T,O,K", [(1, 1024, 2048), (1, 3000, 4096), (1, 2048, 11008), (2, 2048, 8192),
+                                   (4, 2048, 4096), (3, 520, 1024),
                                    (4, 256, 8192), (64, 512, 1024),
                                    (300, 136, 256), (4, 300, 11008), (2, 520, 16384)])
 def test_pow2_bit_exact(T, O, K):
