@@ -7,7 +7,8 @@ GEMM API over torch device tensors, and the INT4 packing/quantisation helpers.
 """
 from ._lib import (  # noqa: F401
     CloveError, CLOVE_ERR_SCRATCH_LIMIT, CLOVE_ERR_WORKSPACE, CLOVE_INT4_GROUPWISE,
-    CLOVE_INT4_REFERENCE_LITERAL, CLOVE_NOALLOC_SCRATCH_BYTES, CLOVE_WORKSPACE_MIN_BYTES,
+    CLOVE_INT4_REFERENCE_LITERAL, CLOVE_INT8_EXACT, CLOVE_INT8_REFERENCE_LITERAL, CLOVE_NOALLOC_SCRATCH_BYTES,
+    CLOVE_WORKSPACE_MIN_BYTES,
 )
 from .gemm import (  # noqa: F401
     INT4_GROUP_SIZE,
@@ -17,6 +18,7 @@ from .gemm import (  # noqa: F401
     gemm_int4,
     gemm_int4_ex,
     gemm_int8,
+    gemm_int8_ex,
     gemm_int8_acc32,
     gemm_int4_group_acc32,
     gemm_int8_rowcol,

@@ -27,6 +27,8 @@ CLOVE_NOALLOC_SCRATCH_BYTES = 32 << 20
 
 CLOVE_INT4_GROUPWISE = 0
 CLOVE_INT4_REFERENCE_LITERAL = 1
+CLOVE_INT8_EXACT = 0
+CLOVE_INT8_REFERENCE_LITERAL = 1
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -41,6 +43,7 @@ SIGNATURES = {
     "clove_gemm_fp16_batched": ([P, P, P, I, I, I, I, F, F, P], I),
     "clove_gemm_fp16_noalloc": ([P, P, P, I, I, I, F, F, P], I),
     "clove_gemm_int8": ([P, P, P, I, I, I, F, I8, F, I8, P], I),
+    "clove_gemm_int8_ex": ([P, P, P, I, I, I, F, I8, F, I8, I, P], I),
     "clove_gemm_int8_rowcol": ([P, P, P, P, P, I, I, I, I8, I8, P], I),
     "clove_gemm_int8_acc32": ([P, P, P, I, I, I, I8, I8, P], I),
     "clove_gemm_int4_group_acc32": ([P, P, P, P, P, I, I, I, P], I),

@@ -4,7 +4,9 @@ Each .hip source under csrc/ is compiled to an object for gfx950 only, then
 linked into clove_compute_amd/lib/libclove_gemm.so.  Objects are rebuilt when
 their source or any header is newer (force=True rebuilds everything).  The
 build then reads every kernel's register and scratch use from the code objects
-(resources.py) and fails if a kernel outside the unaligned fallbacks spills.
+(resources.py) and fails if a kernel outside the unaligned fallbacks spills,
+and scans their disassembly for memory instructions issued without the wait
+states a gfx9 hazard requires (hazards.py).
 """
 from __future__ import annotations
 
@@ -91,8 +93,10 @@ def build(force: bool = False, jobs: int = 8) -> str:
             raise RuntimeError("link of libclove_diag.so failed")
         os.replace(DIAG_LIB + ".tmp", DIAG_LIB)
     # no kernel that an aligned call can reach may spill registers to scratch
-    from clove_compute_amd import resources
+    from clove_compute_amd import hazards, resources
     resources.check(objs + dobjs)
+    # every inline-asm memory instruction has its wait states
+    hazards.check(objs + dobjs)
     return LIB
 
 

@@ -359,6 +359,25 @@ clove_status_t clove_gemm_int8(const int8_t* A_q, const int8_t* B_q, void* C, in
     return int8_common(a, stream);
 }
 
+clove_status_t clove_gemm_int8_ex(const int8_t* A_q, const int8_t* B_q, void* C, int M, int N, int K,
+                                  float A_scale, int8_t A_zero, float B_scale, int8_t B_zero, int mode,
+                                  void* stream) {
+    if (mode != CLOVE_INT8_EXACT && mode != CLOVE_INT8_REFERENCE_LITERAL) return CLOVE_ERR_INVALID_ARG;
+    Int8Args a;
+    a.A = A_q; a.B = B_q; a.C = C; a.M = M; a.N = N; a.K = K;
+    a.scale = A_scale * B_scale;  // combined in fp32 (src/kernels/gemm_int8.cu:40)
+    a.za = A_zero; a.zb = B_zero;
+    if (mode == CLOVE_INT8_REFERENCE_LITERAL && K > 0) {
+        // the reference walks K in 32-wide tiles, loads 0 past K and subtracts
+        // the zero points from it (src/kernels/gemm_int8.cu:43, 52-54, 63-64,
+        // 89-93): each padded k adds za * zb
+        const unsigned pad = (unsigned)(32 * ((K + 31) / 32) - K);
+        a.acc_add = (int)(pad * (unsigned)(int)A_zero * (unsigned)(int)B_zero);
+    }
+    a.out = Int8Out::kHalfPerTensor;
+    return int8_common(a, stream);
+}
+
 clove_status_t clove_gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q, const void* A_scale,
                                       const void* B_scale, void* C, int M, int N, int K,
                                       int8_t A_zero, int8_t B_zero, void* stream) {

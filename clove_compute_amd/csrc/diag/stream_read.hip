@@ -95,7 +95,8 @@ __global__ void __launch_bounds__(kThreads) pull_dma(const unsigned char* src, u
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int soff = s * W * 8192 + i * 1024;
-            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+            // (s_nop: the wait state an LDS DMA needs after the M0 write)
+            asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                          :
                          : "v"(voff), "s"(r), "s"(soff), "{m0}"(st + i * 1024)
                          : "memory");

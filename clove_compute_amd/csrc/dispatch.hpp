@@ -60,6 +60,10 @@ struct Int8Args {
     const uint16_t* sb = nullptr;  // [N] fp16 (kHalfRowCol)
     float scale = 1.0f;            // A_scale * B_scale (kHalfPerTensor)
     int za = 0, zb = 0;
+    // added to every int32 accumulator (wrap-around): (32 ceil(K/32) - K) za zb
+    // in the reference-literal mode, else 0; only the kernels that take zero
+    // points apply it (it is 0 whenever a zero point is)
+    int acc_add = 0;
     int M = 0, N = 0, K = 0;
     Int8Out out = Int8Out::kHalfPerTensor;
 };

@@ -76,8 +76,11 @@ __host__ __device__ constexpr int vmcnt_imm(int n) {
 // compiler does not treat it as a possible writer of the stage being read
 // (it would otherwise wait for every DMA in flight before each LDS read);
 // completion is tracked explicitly with vmcnt + a workgroup barrier.
+// The compiler does not see an LDS DMA inside the asm, so the asm carries the
+// wait state an LDS DMA needs after the SALU write of M0 that the "{m0}"
+// operand places right in front of it (the build's hazard scan checks it).
 __device__ __forceinline__ void dma16(const u32x4& rsrc, unsigned lds_addr, int voff, int soff) {
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                  :
                  : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
                  : "memory");

@@ -37,6 +37,8 @@ struct I8Params {
     const int* colsum;  // [N] sum_k B (only when za != 0)
     float scale;
     int za, zb;
+    int acc_add;  // added to every accumulator (int32 wrap-around): the
+                  // reference-literal mode's padded-k term, else 0
     int M, N, K;
     int tiles_m, tiles_n, nsplit, k_per_split;
     float* ws;
@@ -47,6 +49,7 @@ struct I8Params {
 // the caller before its first store) for kHalfRowCol, else the tensor scale
 template <int OUT>
 __device__ __forceinline__ void int8_store(const I8Params& p, int m, int n, int acc, float s) {
+    acc = (int)((unsigned)acc + (unsigned)p.acc_add);
     if constexpr (OUT == (int)Int8Out::kAcc32) {
         static_cast<int*>(p.C)[(int64_t)m * p.N + n] = acc;
     } else {
@@ -627,7 +630,7 @@ clove_status_t launch_gemm_int8(const Int8Args& a, hipStream_t stream) {
     if (st != CLOVE_OK) return st;
     I8Params p{};
     p.A = a.A; p.B = a.B; p.C = a.C; p.sa = a.sa; p.sb = a.sb;
-    p.scale = a.scale; p.za = a.za; p.zb = a.zb;
+    p.scale = a.scale; p.za = a.za; p.zb = a.zb; p.acc_add = a.acc_add;
     p.M = a.M; p.N = a.N; p.K = a.K;
     const bool aligned = aligned16(a.A) && aligned16(a.B) && (a.K % 16 == 0) && (a.N % 16 == 0);
     // 256x256 tiles once they cover half the CUs (cold weights, against the

@@ -74,7 +74,6 @@ namespace clove {
 namespace i4i4 {
 
 using namespace hw;
-using dma::dma16;
 using dma::make_rsrc;
 using dma::vmcnt_imm;
 
@@ -111,8 +110,21 @@ static_assert(LDS <= 160 * 1024, "LDS");
 static_assert(BR * (BC + 8) * 2 <= BT0 + LB * BST && 4 * 64 * NB * 16 * 4 <= BT0 + LB * BST, "epilogue staging");
 static_assert((LA - 2) * DA <= 63 && (LB - 2) * DB <= 63, "vmcnt range");
 
+// The LDS DMAs of this kernel.  Their asm starts with five wait states: a
+// VMEM instruction that reads an SGPR needs five after a VALU write of it, and
+// the compiler, which does not see the load inside the asm, restores SGPRs it
+// has spilled to VGPR lanes (v_readlane_b32) right in front of the asm (it does
+// in the partials instantiation, whose SGPRs run out).  Without them the load
+// can read a stale resource word: observed as weight rows read as zeros, and a
+// memory fault.  Five wait states also cover the one after the M0 write.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, unsigned lds_addr, int voff, int soff) {
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
+                 : "memory");
+}
 __device__ __forceinline__ void dma4(const u32x4& rsrc, unsigned lds_addr, int voff, int soff) {
-    asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
                  : "memory");

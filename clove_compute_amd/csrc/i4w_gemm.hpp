@@ -115,8 +115,9 @@ __device__ __forceinline__ unsigned lds_read4(unsigned addr) {
     return *reinterpret_cast<const lds_u32*>((size_t)addr);
 }
 
+// (the wait state after the M0 write, as in dma16)
 __device__ __forceinline__ void dma4(const u32x4& rsrc, unsigned lds_addr, int voff, int soff) {
-    asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
                  : "memory");

@@ -70,6 +70,16 @@ def gemm_int8(A_q, B_q, C, M: int, N: int, K: int, A_scale: float, A_zero: int,
                "gemm_int8")
 
 
+def gemm_int8_ex(A_q, B_q, C, M: int, N: int, K: int, A_scale: float, A_zero: int,
+                 B_scale: float, B_zero: int, mode: int = 0, stream=None) -> None:
+    """gemm_int8 with an arithmetic mode: CLOVE_INT8_EXACT (0), or
+    CLOVE_INT8_REFERENCE_LITERAL (1), the reference kernel's accumulator at any K
+    (each zero-padded k of its last 32-wide K tile adds A_zero * B_zero)."""
+    _lib.check(_lib.lib().clove_gemm_int8_ex(_ptr(A_q), _ptr(B_q), _ptr(C), M, N, K, A_scale,
+                                             A_zero, B_scale, B_zero, mode, _stream(stream)),
+               "gemm_int8_ex")
+
+
 def gemm_int8_rowcol(A_q, B_q, A_scale, B_scale, C, M: int, N: int, K: int,
                      A_zero: int = 0, B_zero: int = 0, stream=None) -> None:
     _lib.check(_lib.lib().clove_gemm_int8_rowcol(_ptr(A_q), _ptr(B_q), _ptr(A_scale),

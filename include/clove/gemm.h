@@ -114,6 +114,13 @@ inline void gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q, const half* A
                                               B_zero, stream));
 }
 
+inline void gemm_int8_ex(const int8_t* A_q, const int8_t* B_q, half* C, int M, int N, int K,
+                         float A_scale, int8_t A_zero, float B_scale, int8_t B_zero,
+                         clove_int8_mode_t mode, hipStream_t stream = 0) {
+    CLOVE_CHECK_STATUS(clove_gemm_int8_ex(A_q, B_q, C, M, N, K, A_scale, A_zero, B_scale,
+                                          B_zero, (int)mode, stream));
+}
+
 inline void gemm_int4_ex(const uint8_t* A_q, const half* A_scale, const half* A_zero,
                          const uint8_t* B_q, const half* B_scale, const half* B_zero, half* C,
                          int M, int N, int K, clove_int4_mode_t mode, hipStream_t stream = 0) {

@@ -98,6 +98,27 @@ clove_status_t clove_gemm_int8(const int8_t* A_q, const int8_t* B_q, void* C,
                                float A_scale, int8_t A_zero,
                                float B_scale, int8_t B_zero, void* stream);
 
+/* INT8 arithmetic modes of clove_gemm_int8_ex */
+typedef enum {
+    /* acc = sum over k < K only (clove_gemm_int8) */
+    CLOVE_INT8_EXACT = 0,
+    /* the reference kernel's accumulator at any K: it walks K in 32-wide tiles,
+     * loads 0 for k >= K and subtracts the zero points from those zeros too, so
+     * acc = exact + (32*ceil(K/32) - K) * A_zero * B_zero
+     * (src/kernels/gemm_int8.cu:43, 52-54, 63-64, 89-93); equal to
+     * CLOVE_INT8_EXACT when K % 32 == 0 or a zero point is 0 */
+    CLOVE_INT8_REFERENCE_LITERAL = 1
+} clove_int8_mode_t;
+
+/*
+ * clove_gemm_int8 with a choice of arithmetic mode (clove_int8_mode_t).
+ * Extension of clove::gemm_int8 (include/clove/kernels/gemm.cuh:57-65).
+ */
+clove_status_t clove_gemm_int8_ex(const int8_t* A_q, const int8_t* B_q, void* C,
+                                  int M, int N, int K,
+                                  float A_scale, int8_t A_zero,
+                                  float B_scale, int8_t B_zero, int mode, void* stream);
+
 /*
  * W8A8 with fp16 per-row scales A_scale [M] (tokens) and per-column scales
  * B_scale [N] (output channels): C = fp16(float(acc) * (A_scale[m]*B_scale[n])).

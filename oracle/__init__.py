@@ -51,6 +51,7 @@ def lib():
             "oracle_gemm_fp16_f64": ([P, P, P, P, I, I, I, D, D], None),
             "oracle_gemm_fp16_batched": ([P, P, P, I, I, I, I, F, F], None),
             "oracle_gemm_int8": ([P, P, P, P, I, I, I, F, ctypes.c_int8, F, ctypes.c_int8], None),
+            "oracle_gemm_int8_literal": ([P, P, P, P, I, I, I, F, ctypes.c_int8, F, ctypes.c_int8], None),
             "oracle_gemm_int8_rowcol": ([P, P, P, P, P, P, I, I, I, ctypes.c_int8, ctypes.c_int8], None),
             "oracle_gemm_int4_literal": ([P, P, P, P, P, I, I, I], None),
             "oracle_gemm_int4_groupwise": ([P, P, P, P, P, P, P, P, P, I, I, I], None),
@@ -155,6 +156,20 @@ def gemm_int8(A_q, B_q, A_scale, A_zero, B_scale, B_zero):
     acc = np.empty((M, N), np.int32)
     lib().oracle_gemm_int8(_p(A_q), _p(B_q), _p(C), _p(acc), M, N, K,
                            float(A_scale), int(A_zero), float(B_scale), int(B_zero))
+    return C, acc
+
+
+def gemm_int8_literal(A_q, B_q, A_scale, A_zero, B_scale, B_zero):
+    """The reference kernel's arithmetic at any K (padded k of the last 32-wide
+    tile contribute A_zero * B_zero).  Returns (C fp16 [M,N], acc int32 [M,N])."""
+    A_q = _c(A_q, np.int8)
+    B_q = _c(B_q, np.int8)
+    M, K = A_q.shape
+    N = B_q.shape[1]
+    C = np.empty((M, N), np.float16)
+    acc = np.empty((M, N), np.int32)
+    lib().oracle_gemm_int8_literal(_p(A_q), _p(B_q), _p(C), _p(acc), M, N, K,
+                                   float(A_scale), int(A_zero), float(B_scale), int(B_zero))
     return C, acc
 
 

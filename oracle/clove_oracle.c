@@ -266,6 +266,36 @@ void oracle_gemm_int8(const int8_t* A_q, const int8_t* B_q, uint16_t* C,
     free(acc);
 }
 
+/* The reference kernel's own arithmetic at any K, as its owning block runs it
+ * (src/kernels/gemm_int8.cu:43-96): K is walked in 32-wide tiles (:43), bytes
+ * at k >= K are loaded as 0 (:52-54, :63-64), and the zero points are
+ * subtracted from every loaded byte (:89-93), so each of the 32*ceil(K/32) - K
+ * padded k of the last tile adds (0 - A_zero) * (0 - B_zero).  Epilogue as
+ * oracle_gemm_int8 (:40, :113-114). */
+void oracle_gemm_int8_literal(const int8_t* A_q, const int8_t* B_q, uint16_t* C,
+                              int32_t* acc_out, int M, int N, int K,
+                              float A_scale, int8_t A_zero, float B_scale, int8_t B_zero) {
+    if (M <= 0 || N <= 0) return;
+    const int BK = 32;
+    const float combined = A_scale * B_scale;
+    for (int m = 0; m < M; m++) {
+        for (int n = 0; n < N; n++) {
+            uint32_t acc = 0; /* int32 with wrap-around, like the reference's int */
+            for (int k0 = 0; k0 < K; k0 += BK) {
+                for (int kk = 0; kk < BK; kk++) {
+                    const int k = k0 + kk;
+                    const int a = k < K ? A_q[(int64_t)m * K + k] : 0;
+                    const int b = k < K ? B_q[(int64_t)k * N + n] : 0;
+                    acc += (uint32_t)((a - (int)A_zero) * (b - (int)B_zero));
+                }
+            }
+            const int64_t i = (int64_t)m * N + n;
+            if (C) C[i] = oracle_f32_to_f16((float)(int32_t)acc * combined);
+            if (acc_out) acc_out[i] = (int32_t)acc;
+        }
+    }
+}
+
 /* Row/column-scale extension of the same formula: combined = sa[m] * sb[n]. */
 void oracle_gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q,
                              const uint16_t* sa, const uint16_t* sb, uint16_t* C,

@@ -74,6 +74,13 @@ void oracle_gemm_int8(const int8_t* A_q, const int8_t* B_q, uint16_t* C,
                       int32_t* acc_out, int M, int N, int K,
                       float A_scale, int8_t A_zero, float B_scale, int8_t B_zero);
 
+/* W8A8 as the reference kernel computes it at any K: 32-wide K tiles whose
+ * bytes past K load as 0 before the zero points are subtracted, so every padded
+ * k adds A_zero * B_zero (gemm_int8.cu:43-96). */
+void oracle_gemm_int8_literal(const int8_t* A_q, const int8_t* B_q, uint16_t* C,
+                              int32_t* acc_out, int M, int N, int K,
+                              float A_scale, int8_t A_zero, float B_scale, int8_t B_zero);
+
 /* W8A8 with fp16 per-row scales sa [M] and per-column scales sb [N]. */
 void oracle_gemm_int8_rowcol(const int8_t* A_q, const int8_t* B_q,
                              const uint16_t* sa, const uint16_t* sb, uint16_t* C,

@@ -195,6 +195,24 @@ def test_int8_mfma_path_zero_point_range_bit_exact(M, N, K):
     assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))
 
 
+@pytest.mark.parametrize("M,K", [(4096, 11008), (11008, 4096)])
+def test_int8_mfma_path_config4_n128_every_row_bit_exact(M, K):
+    # the config-4 prefill shapes on the int8-MFMA kernel, every row and
+    # column: power-of-two scales and q - z in [-1, 1], so every per-group
+    # sum, scale product and fp32 fold is exact and the output is the fp16
+    # rounding of the exact value (computed here in float64, group by group)
+    N = 128
+    A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2-cfg4", pow2=True, small=True)
+    C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
+    G = K // 128
+    a = quant.unpack_rows(A_q, K).astype(np.float64).reshape(M, G, 128) - zA.astype(np.float64)[:, :, None]
+    b = quant.unpack_cols(B_q, N).astype(np.float64).reshape(G, 128, N) - zB.astype(np.float64)[:, None, :]
+    ref = np.zeros((M, N))
+    for g in range(G):
+        ref += sA[:, g, None].astype(np.float64) * sB[None, g, :].astype(np.float64) * (a[:, g, :] @ b[g])
+    assert np.array_equal(f16bits(C), f16bits(ref.astype(np.float16)))
+
+
 def test_int8_mfma_path_zero_point_outside_range_is_nan():
     # a zero point the int8 operands cannot hold exactly poisons exactly the
     # outputs whose sum it enters (its row, or its column), nothing else
@@ -249,19 +267,13 @@ def partials_int64(A_q, zA, B_q, zB, rows, N, K):
     return np.einsum("rgk,gkn->rng", a, b)
 
 
-# The partials hook stays off the GPU: a GPU run of this file ended with the GPU
-# faulted and test_group_partials_bit_exact[130-64-512] failing, and reading
-# the hook's path (i4_prep_bt with no scales, i4i4_gemm<true>: every DMA range,
-# LDS offset and guarded store) has not shown a cause.  The product kernel it
-# shares its loop with keeps its GPU tests above.
-PARTIALS_OFF = pytest.mark.skip(reason="a GPU run failed here and ended with the GPU faulted; no cause found yet")
-
-
-# The int8-MFMA kernel's per-group integer sums P_g, through the partials hook:
+# The int8-MFMA kernel's per-group integer sums P_g, through the partials hook
+# (its LDS DMAs carry their own wait states: without them the compiled hook
+# read weight rows as zeros after restoring a spilled resource SGPR, see
+# tests/test_hazards.py):
 # bit for bit against the oracle's partials and an independent numpy int64
 # restatement, with arbitrary zero points over the kernel's whole exact range
 # [-112, 127] (not only 8) and ragged M / N.
-@PARTIALS_OFF
 @pytest.mark.parametrize("M,N,K", [(130, 64, 512), (64, 1, 256), (257, 200, 1024), (1000, 128, 11008)])
 def test_group_partials_bit_exact(M, N, K):
     g = rng("i4-partials", M, N, K)
@@ -281,7 +293,6 @@ def test_group_partials_bit_exact(M, N, K):
         assert np.array_equal(P, part)
 
 
-@PARTIALS_OFF
 def test_group_partials_zero_point_outside_range():
     # a zero point the int8 operands cannot hold marks exactly the partials of
     # its row (or column) and group with INT32_MIN

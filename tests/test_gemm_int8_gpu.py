@@ -74,6 +74,35 @@ def test_per_tensor_bit_exact(M, N, K, za, zb):
     assert np.array_equal(run_acc32(A, B, za, zb), accref)
 
 
+# The reference kernel's own accumulator at ragged K (CLOVE_INT8_REFERENCE_LITERAL):
+# each zero-padded k of its last 32-wide K tile adds A_zero * B_zero
+# (src/kernels/gemm_int8.cu:52-54, 63-64, 89-93).  Bit for bit against the
+# oracle's restatement of that tile loop, on the GEMV (M <= 4) and MFMA routes;
+# with K % 32 == 0 or a zero point 0 the mode equals the exact one.
+@pytest.mark.parametrize("M,N,K,za,zb", [
+    (1, 512, 1000, 3, -5), (200, 130, 300, 5, -9), (37, 19, 45, 1, 1), (4, 96, 70, 7, 7),
+    (129, 4096, 520, -3, 2), (64, 64, 64, 4, 4), (33, 40, 100, 0, 9),
+])
+def test_reference_literal_mode_bit_exact(M, N, K, za, zb):
+    g = rng("lit8", M, N, K, za, zb)
+    A = g.integers(-128, 128, (M, K)).astype(np.int8)
+    B = g.integers(-128, 128, (K, N)).astype(np.int8)
+    sa, sb = np.float32(g.uniform(0.001, 0.05)), np.float32(g.uniform(0.001, 0.05))
+    cg = _cg()
+    C = empty_f16(M, N)
+    cg.gemm_int8_ex(to_dev(A), to_dev(B), C, M, N, K, float(sa), za, float(sb), zb,
+                    cg.CLOVE_INT8_REFERENCE_LITERAL)
+    Ce = empty_f16(M, N)
+    cg.gemm_int8_ex(to_dev(A), to_dev(B), Ce, M, N, K, float(sa), za, float(sb), zb, cg.CLOVE_INT8_EXACT)
+    _sync()
+    Clit, _ = oracle.gemm_int8_literal(A, B, sa, za, sb, zb)
+    Cex, _ = oracle.gemm_int8(A, B, sa, za, sb, zb)
+    assert np.array_equal(f16bits(to_host(C)), f16bits(Clit))
+    assert np.array_equal(f16bits(to_host(Ce)), f16bits(Cex))
+    if (32 * ((K + 31) // 32) - K) * za * zb == 0:
+        assert np.array_equal(f16bits(Clit), f16bits(Cex))
+
+
 def test_reference_race_region_is_correct():
     # the reference kernel's 64x64 tiles let threads write outside their tile
     # (src/kernels/gemm_int8.cu:29-34 vs :9-10); every element here must equal

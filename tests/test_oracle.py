@@ -193,6 +193,41 @@ def test_int8_rowcol_and_per_tensor_agree():
     assert np.array_equal(f16bits(Cr), f16bits(Ct))
 
 
+@pytest.mark.parametrize("M,N,K,za,zb", [(37, 19, 45, 1, 1), (1, 512, 1000, 3, -5), (200, 130, 300, 5, -9),
+                                          (9, 7, 64, 4, 3), (5, 6, 33, 0, 7), (5, 6, 33, -8, 0)])
+def test_int8_reference_literal(M, N, K, za, zb):
+    # the reference kernel at ragged K: each of the 32 * ceil(K / 32) - K
+    # zero-padded k of its last 32-wide tile adds (0 - za)(0 - zb) to the
+    # accumulator (src/kernels/gemm_int8.cu:52-54, 63-64, 89-93); pinned against
+    # the exact sum plus that closed-form term, numpy int64
+    A = RNG.integers(-128, 128, (M, K)).astype(np.int8)
+    B = RNG.integers(-128, 128, (K, N)).astype(np.int8)
+    sa, sb = np.float32(0.0123), np.float32(0.0071)
+    Cl, accl = oracle.gemm_int8_literal(A, B, sa, za, sb, zb)
+    Ce, acce = oracle.gemm_int8(A, B, sa, za, sb, zb)
+    exact = (A.astype(np.int64) - za) @ (B.astype(np.int64) - zb)
+    pad = 32 * ((K + 31) // 32) - K
+    assert np.array_equal(acce.astype(np.int64), exact)
+    assert np.array_equal(accl.astype(np.int64), exact + pad * za * zb)
+    cs = np.float32(sa * sb)
+    lit = ((exact + pad * za * zb).astype(np.float32) * cs).astype(np.float16)
+    assert np.array_equal(f16bits(Cl), f16bits(lit))
+    if pad * za * zb == 0:  # K % 32 == 0 or a zero point 0: the two agree
+        assert np.array_equal(f16bits(Cl), f16bits(Ce))
+    else:
+        assert np.all(accl.astype(np.int64) - acce.astype(np.int64) == pad * za * zb)
+
+
+def test_int8_reference_literal_difference_at_37x19x45():
+    # K = 45: the last tile holds 19 padded k, so with zero points (1, 1) the
+    # reference's accumulator is the exact sum + 19
+    A = RNG.integers(-128, 128, (37, 45)).astype(np.int8)
+    B = RNG.integers(-128, 128, (45, 19)).astype(np.int8)
+    _, accl = oracle.gemm_int8_literal(A, B, 1.0, 1, 1.0, 1)
+    _, acce = oracle.gemm_int8(A, B, 1.0, 1, 1.0, 1)
+    assert np.all(accl.astype(np.int64) - acce == 19)
+
+
 # ---------------------------------------------------------------------------
 # INT4
 # ---------------------------------------------------------------------------
