@@ -29,11 +29,21 @@ The shapes are timed as HIP-graph replays of one call per operand copy: the
 copies rotate through >= 512 MiB so that no call finds its weights in the
 256 MB Infinity Cache (cold), and the graph removes the per-call host launch
 cost, which exceeds most of these kernels' run time.  Each graph is checked
-once against the same calls run eagerly.  `us` is graph time per call (kernel
-plus the inter-kernel gap); `us_hot` replays one copy.  INT4 W4A4 is priced
-at the INT8 MFMA peak (its integer products fit i8 operands).
+once against the same calls run eagerly, and the first call's output on a few
+rows against the oracle (`parity`: bit-exact for INT8, the tolerance of the
+GPU tests otherwise; a mismatch stops the run).  `us` is graph time per call
+(kernel plus the inter-kernel gap); `us_hot` replays one copy.  INT4 W4A4 is
+priced at the INT8 MFMA peak (its integer products fit i8 operands).  With
+--compare-lib every FP16 shape is also timed through torch.matmul (hipBLASLt)
+and INT8 M > 16 through torch._int_mm on the same operands (`lib_us`).
+
+`device.sclk_mhz_measured` is the shader clock under the headline's load (a
+probe wave after each launch counts shader cycles against the 100 MHz
+constant counter), and `roofline.frac_at_measured_sclk` the headline against
+the dense peak at that clock.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+                       [--skip-extra] [--compare-lib] [--floor]
 """
 from __future__ import annotations
 
@@ -93,12 +103,12 @@ class Timer:
         return self.s.elapsed_time(self.e) / steps  # ms per call
 
 
-def graph_time(calls, outputs, replays=5):
+def graph_time(calls, outputs, replays=5, compare=True):
     """Captures calls[0..n) into one HIP graph on a private stream (after an
     eager pass on that stream, which also allocates any split-K scratch for it)
     and returns the mean time per call in microseconds over `replays` replays.
     The first replay's outputs must equal the eager ones bit for bit (the
-    kernels are deterministic)."""
+    kernels are deterministic; `compare=False` for a library's calls)."""
     import torch
     s = torch.cuda.Stream()
     torch.cuda.synchronize()  # operands were generated on the default stream
@@ -118,7 +128,7 @@ def graph_time(calls, outputs, replays=5):
             o.zero_()
         g.replay()
         torch.cuda.synchronize()
-        for o, e in zip(outputs, eager):
+        for o, e in zip(outputs if compare else [], eager):
             if not torch.equal(o.view(torch.int16), e.view(torch.int16)):
                 raise RuntimeError("graph replay differs from the eager calls")
         g.replay()
@@ -148,6 +158,45 @@ def headline(args, timer):
     ms = timer.run(lambda i: cg.gemm_fp16(A, B, C, M, N, K), args.steps, args.warmup)
     tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     return dict(ms=ms, tflops=tflops, A=A_h, B=B_h, C=C, dA=A, dB=B)
+
+
+def diag_lib():
+    import ctypes
+    path = os.path.join(ROOT, "clove_compute_amd", "lib", "libclove_diag.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+    return ctypes.CDLL(path)
+
+
+def measure_sclk(h, steps, ticks=200):
+    """The shader clock under the headline's load: `steps` launches of the
+    headline GEMM on torch's current stream, each followed by a probe wave
+    (libclove_diag.so sclk_probe) that counts shader cycles over `ticks` of
+    the 100 MHz constant counter (2 us), right after the GEMM drains.  Returns
+    the median, min and max in MHz over the probes."""
+    import ctypes
+
+    import torch
+
+    import clove_compute_amd as cg
+    lib = diag_lib()
+    lib.clove_diag_sclk.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_void_p]
+    lib.clove_diag_sclk.restype = ctypes.c_int
+    A, B, C = h["dA"], h["dB"], h["C"]
+    n = 4096
+    buf = torch.zeros(steps, 4, dtype=torch.int64, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in range(steps):
+        cg.gemm_fp16(A, B, C, n, n, n)
+        if lib.clove_diag_sclk(ctypes.c_void_p(buf[i].data_ptr()), ticks, stream) != 0:
+            raise RuntimeError("clove_diag_sclk failed")
+    torch.cuda.synchronize()
+    v = buf.cpu().tolist()
+    mhz = sorted(100.0 * (c1 - c0) / (r1 - r0) for c0, r0, c1, r1 in v if r1 > r0)
+    if not mhz:
+        return None
+    return {"median": round(mhz[len(mhz) // 2], 1), "min": round(mhz[0], 1), "max": round(mhz[-1], 1),
+            "probes": len(mhz)}
 
 
 def compare_library(h, timer, steps, warmup, rounds=3):
@@ -264,12 +313,53 @@ def copies_for(nbytes):
     return max(2, -(-ROTATE_BYTES // max(1, nbytes)))
 
 
-def extras():
+def pick_rows(n, count=4):
+    """A few row indices spread over [0, n): the first, the last and some between."""
+    return sorted({0, n - 1, n // 3, (2 * n) // 3, n // 2}) if n > 1 else [0]
+
+
+def extras(compare_lib=False):
     """Every shape of the five named configurations except the headline, each
-    timed as graph replays with cold weights.  Returns {name: figures}."""
+    timed as graph replays with cold weights and its first call's output
+    checked on a few rows against the oracle.  Returns {name: figures}."""
+    import numpy as np
     import torch
 
     import clove_compute_amd as cg
+    import oracle
+    from tests._util import f16bits, to_host, within_tol
+
+    def host(t):
+        return to_host(t) if t.dtype == torch.float16 else t.cpu().numpy()
+
+    def tol(got, ref64):
+        ok, rep = within_tol(got, ref64)
+        if not ok:
+            raise RuntimeError(f"parity check failed: {rep}")
+        return f"ok: max rel err {rep['max_rel_err_floored']:.2e} (bound 1e-2)"
+
+    def chk_fp16(x, B, C, M):
+        rows = pick_rows(M)
+        return lambda: tol(host(C)[rows], oracle.gemm_fp16_f64(host(x)[rows], host(B)))
+
+    def chk_int8(a8, B, sa, sb, C, M):
+        rows = pick_rows(M)
+
+        def f():
+            ref, _ = oracle.gemm_int8_rowcol(host(a8)[rows], host(B), host(sa)[rows], host(sb))
+            if not np.array_equal(f16bits(host(C)[rows]), f16bits(ref)):
+                raise RuntimeError("parity check failed: INT8 output differs from the oracle")
+            return "ok: bit-exact"
+        return f
+
+    def chk_int4(s, Bq, Bsc, Bz, C, M, N, K):
+        rows = pick_rows(M)
+
+        def f():
+            Aq, sA, zA = (host(t)[rows] for t in s)
+            _, ref, _ = oracle.gemm_int4_groupwise(Aq, sA, zA, host(Bq), host(Bsc), host(Bz), len(rows), N, K)
+            return tol(host(C)[rows], ref)
+        return f
 
     gen = torch.Generator(device="cuda")
 
@@ -299,7 +389,12 @@ def extras():
 
     out = {}
 
-    def record(name, calls, outputs, flops, nbytes, peak, hot_calls=None, replays=5):
+    def record(name, calls, outputs, flops, nbytes, peak, hot_calls=None, replays=5, check=None,
+               lib_calls=None, lib_outputs=None):
+        """Times `calls`, then checks the outputs of the first call against the
+        oracle (`check()` raises on a mismatch, so no wrong kernel yields a
+        timed number) and, with --compare-lib, times the library's calls on the
+        same operands the same way."""
         us = graph_time(calls, outputs, replays)
         t_mfma = flops / (peak * 1e6)
         t_hbm = nbytes / (PEAK_HBM_GBS * 1e3)
@@ -308,23 +403,39 @@ def extras():
                  bound="mfma" if t_mfma >= t_hbm else "hbm", t_roof_us=t_roof, frac_roofline=t_roof / us)
         if hot_calls is not None:
             d["us_hot"] = graph_time(hot_calls, outputs[:1], replays)
+        if check is not None:
+            d["parity"] = check()
+        if lib_calls is not None and compare_lib:
+            try:
+                lus = graph_time(lib_calls, lib_outputs or [], replays, compare=False)
+                d["lib_us"] = lus
+                d["lib_vs_clove"] = lus / us
+            except Exception as e:  # a library without this shape
+                d["lib_us"] = None
+                d["lib_error"] = str(e).splitlines()[0][:120]
         out[name] = d
-        print(f"[bench] {name}: {us:.2f} us", file=sys.stderr, flush=True)
+        print(f"[bench] {name}: {us:.2f} us" + (f" (library {d['lib_us']:.2f} us)" if d.get("lib_us") else ""),
+              file=sys.stderr, flush=True)
 
     # ---- FP16: 512^3 (U[-1,1]) and the decode/prefill rows of the LLM shapes ----
     A5, B5 = u16((512, 512), 1), u16((512, 512), 2)
     C5 = torch.empty(512, 512, dtype=torch.float16, device="cuda")
+    L5 = torch.empty_like(C5)
     c = [lambda: cg.gemm_fp16(A5, B5, C5, 512, 512, 512)] * 16
-    record("fp16_512x512x512", c, [C5], 2 * 512 ** 3, 2 * 3 * 512 * 512, PEAK_FP16_TFLOPS)
+    record("fp16_512x512x512", c, [C5], 2 * 512 ** 3, 2 * 3 * 512 * 512, PEAK_FP16_TFLOPS,
+           check=chk_fp16(A5, B5, C5, 512), lib_calls=[lambda: torch.matmul(A5, B5, out=L5)] * 16)
     for M in (1, 32, 128):
         N = K = 4096
         x = f16((M, K), 1.0, 3 + M)
         Bs = [f16((K, N), 0.02, 100 + i) for i in range(copies_for(K * N * 2))]
         Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
         calls = [lambda B=B, C=C, M=M: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
+        Ls = [torch.empty_like(C) for C in Cs] if compare_lib else []
+        lcalls = [lambda B=B, L=L: torch.matmul(x, B, out=L) for B, L in zip(Bs, Ls)]
         record(f"fp16_{M}x4096x4096", calls, Cs, 2 * M * N * K, 2 * (M * K + K * N + M * N),
-               PEAK_FP16_TFLOPS, hot_calls=calls[:1] * 16 if M == 1 else None)
-        del Bs, Cs, calls
+               PEAK_FP16_TFLOPS, hot_calls=calls[:1] * 16 if M == 1 else None,
+               check=chk_fp16(x, Bs[0], Cs[0], M), lib_calls=lcalls)
+        del Bs, Cs, calls, Ls, lcalls
 
     # ---- the reference benchmark's other FP16 shapes (bench/bench_gemm.cu:20-37):
     # (M, N, K) with activations ~N(0,1) and weights ~N(0,0.02), weights cold ----
@@ -334,9 +445,11 @@ def extras():
         Bs = [f16((K, N), 0.02, 140 + i) for i in range(copies_for(K * N * 2))]
         Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
         calls = [lambda B=B, C=C, M=M, N=N, K=K: cg.gemm_fp16(x, B, C, M, N, K) for B, C in zip(Bs, Cs)]
+        Ls = [torch.empty_like(C) for C in Cs] if compare_lib else []
+        lcalls = [lambda B=B, L=L: torch.matmul(x, B, out=L) for B, L in zip(Bs, Ls)]
         record(f"ref_bench_fp16_{M}x{N}x{K}", calls, Cs, 2 * M * N * K, 2 * (M * K + K * N + M * N),
-               PEAK_FP16_TFLOPS)
-        del Bs, Cs, calls
+               PEAK_FP16_TFLOPS, check=chk_fp16(x, Bs[0], Cs[0], M), lib_calls=lcalls)
+        del Bs, Cs, calls, Ls, lcalls
 
     # ---- INT8 W8A8 with per-row / per-column fp16 scales: the decode / small
     # batch rows of config 3 (weights cold), and the prefill square 4096^3 ----
@@ -348,9 +461,13 @@ def extras():
         Bs = [i8((K, N), 500 + i) for i in range(copies_for(K * N))]
         Cs = [torch.empty(M, N, dtype=torch.float16, device="cuda") for _ in Bs]
         calls = [lambda B=B, C=C, M=M: cg.gemm_int8_rowcol(a8, B, sa, sb, C, M, N, K) for B, C in zip(Bs, Cs)]
+        # the library's int8 GEMM (int32 out, no scale epilogue; hipBLASLt
+        # takes M > 16 only)
+        Ls = [torch.empty(M, N, dtype=torch.int32, device="cuda") for _ in Bs] if compare_lib and M > 16 else []
+        lcalls = [lambda B=B, L=L: torch._int_mm(a8, B, out=L) for B, L in zip(Bs, Ls)] if Ls else None
         record(f"int8_{M}x4096x4096", calls, Cs, 2 * M * N * K, M * K + K * N + 2 * M * N + 2 * M + 2 * N,
-               PEAK_INT8_TOPS)
-        del Bs, Cs, calls
+               PEAK_INT8_TOPS, check=chk_int8(a8, Bs[0], sa, sb, Cs[0], M), lib_calls=lcalls)
+        del Bs, Cs, calls, Ls, lcalls
 
     # ---- INT4 W4A4 group-wise: weights A_q [M, K/2], activations B_q [K, ceil(N/2)] ----
     for (M, K) in ((11008, 4096), (4096, 11008)):
@@ -367,7 +484,8 @@ def extras():
                      for s, C in zip(sets, Cs)]
             nb = wbytes + K * ((N + 1) // 2) + 4 * G * N + 2 * M * N
             record(f"int4_w4a4_{M}x{K}_n{N}", calls, Cs, 2 * M * N * K, nb, PEAK_INT8_TOPS,
-                   hot_calls=calls[:1] * 16 if N == 1 else None)
+                   hot_calls=calls[:1] * 16 if N == 1 else None,
+                   check=chk_int4(sets[0], Bq, Bsc, Bz, Cs[0], M, N, K))
             del Cs, calls
         del sets
 
@@ -412,19 +530,42 @@ def extras():
             cg.w4a16_swiglu(x, *L[2], h, T, inter, hid)
             cg.gemm_w4a16(h, *L[3], res, T, hid, inter, 1.0, 1.0)
 
+        def chk_layer(L, fused, T=T):
+            # one eager step on the first copy, then the QKV output and the MLP
+            # activation h on a few tokens against the oracle (the residual
+            # outputs accumulate across calls and are not compared)
+            rows = pick_rows(T)
+
+            def f():
+                (step_fused if fused else step)(L)
+                torch.cuda.synchronize()
+                xr = host(x)[rows]
+                _, q64 = oracle.w4a16(xr, *(host(t) for t in L[0]))
+                r = [tol(host(q)[rows], q64)]
+                if fused:
+                    href = oracle.w4a16_swiglu(xr, *(host(t) for t in L[2]))
+                else:
+                    g_, _ = oracle.w4a16(xr, *(host(t) for t in L[2]))
+                    u_, _ = oracle.w4a16(xr, *(host(t) for t in L[3]))
+                    href = oracle.swiglu(g_, u_)
+                r.append(tol(host(h)[rows], href.astype(np.float64)))
+                return "; ".join(r)
+            return f
+
         flops = sum(2 * T * O * K for O, K, _ in layer)
         lin = sum(2 * T * K + 2 * T * O * (2 if b else 1) for O, K, b in layer)
         # the residual projections accumulate into res across calls: compare the
         # other outputs only
         calls = [lambda L=L: step(L) for L in layers]
         record(f"w4a16_llama1b_layer_T{T}", calls, [q, gate, up, h], flops,
-               wbytes + lin + 3 * 2 * T * inter, PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3)
+               wbytes + lin + 3 * 2 * T * inter, PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3,
+               check=chk_layer(layers[0], False))
         fused = [fuse_gate_up(L) for L in layers]
         del layers, calls
         calls = [lambda L=L: step_fused(L) for L in fused]
         lin_f = lin - 2 * (2 * T * hid + 2 * T * inter) + (2 * T * hid + 2 * T * inter)
         record(f"w4a16_llama1b_layer_fused_T{T}", calls, [q, h], flops, wbytes + lin_f,
-               PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3)
+               PEAK_FP16_TFLOPS, replays=5 if T == 1 else 3, check=chk_layer(fused[0], True))
         del fused, calls
 
     # ---- FP16 Llama-1B MLP: gate / up projections and SwiGLU on FP16 weights
@@ -437,9 +578,19 @@ def extras():
         pairs = [(f16((H, I), 0.02, 960 + 2 * i), f16((H, I), 0.02, 961 + 2 * i)) for i in range(copies_for(wb))]
         outs = [torch.empty(T, I, dtype=torch.float16, device="cuda") for _ in pairs]
         flops = 2 * 2 * T * H * I
+
+        def chk_mlp(w, o, T=T):
+            rows = pick_rows(T)
+
+            def f():
+                xr = host(x)[rows]
+                g_ = oracle.gemm_fp16_f64(xr, host(w[0])).astype(np.float16)
+                u_ = oracle.gemm_fp16_f64(xr, host(w[1])).astype(np.float16)
+                return tol(host(o)[rows], oracle.swiglu(g_, u_).astype(np.float64))
+            return f
         calls = [lambda w=w, o=o, T=T: cg.swiglu_fused(x, w[0], w[1], o, T, H, I) for w, o in zip(pairs, outs)]
         record(f"fp16_llama1b_mlp_swiglu_fused_T{T}", calls, outs, flops, wb + 2 * T * H + 2 * T * I,
-               PEAK_FP16_TFLOPS)
+               PEAK_FP16_TFLOPS, check=chk_mlp(pairs[0], outs[0]))
         gate = torch.empty(T, I, dtype=torch.float16, device="cuda")
         up = torch.empty_like(gate)
 
@@ -449,7 +600,7 @@ def extras():
             cg.swiglu(gate, up, o, T * I)
         calls = [lambda w=w, o=o: unfused(w, o) for w, o in zip(pairs, outs)]
         record(f"fp16_llama1b_mlp_unfused_T{T}", calls, outs, flops,
-               wb + 2 * 2 * T * H + 3 * 2 * 2 * T * I, PEAK_FP16_TFLOPS)
+               wb + 2 * 2 * T * H + 3 * 2 * 2 * T * I, PEAK_FP16_TFLOPS, check=chk_mlp(pairs[0], outs[0]))
         del pairs, outs, calls
     return out
 
@@ -463,10 +614,7 @@ def floor():
     import ctypes
 
     import torch
-    path = os.path.join(ROOT, "clove_compute_amd", "lib", "libclove_diag.so")
-    if not os.path.exists(path):
-        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
-    lib = ctypes.CDLL(path)
+    lib = diag_lib()
     lib.clove_diag_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
     lib.clove_diag_stream_read.restype = ctypes.c_int
     sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
@@ -580,11 +728,21 @@ def main():
                      "traffic": traffic, "flops_per_launch": flops,
                      "kernel": "dma::gemm_f16_big<Big>"},
     }
+    # the clock the headline ran at, and its fraction of the dense peak at that
+    # clock (256 CUs x 4096 flop/clk x the measured shader clock)
+    clk = measure_sclk(h, max(args.steps, 20))
+    if clk is not None:
+        line["device"]["sclk_mhz_measured"] = clk
+        line["device"]["sclk_method"] = ("s_memtime / s_memrealtime probe wave after each of the headline "
+                                         "GEMM's launches (libclove_diag.so clove_diag_sclk)")
+        peak_at = 256 * 4096 * clk["median"] * 1e6 / 1e12
+        line["roofline"]["peak_at_measured_sclk"] = round(peak_at, 1)
+        line["roofline"]["frac_at_measured_sclk"] = round(achieved / peak_at, 4)
     if args.compare_lib:
         line["library_comparison"] = compare_library(h, timer, args.steps, args.warmup)
     if not args.skip_extra:
         line["shapes"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                          for k, v in extras().items()}
+                          for k, v in extras(args.compare_lib).items()}
     if args.cpu_seconds > 0:
         cb = cpu_baseline(h, args.cpu_seconds)
         cb["value"] = round(cb["value"], 6)

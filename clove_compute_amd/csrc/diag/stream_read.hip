@@ -1,7 +1,8 @@
 // Diagnostic, not part of the GEMM C-ABI: read-only streaming kernels that
 // measure the cold HBM read floor the memory-bound GEMM kernels are compared
 // with, and how fast one CU pulls data by each load kind the kernels use.
-// Built into lib/libclove_diag.so and used by bench.py --floor only.
+// Built into lib/libclove_diag.so and used by bench.py --floor, and the shader
+// clock probe (sclk_probe) bench.py runs between launches of the headline GEMM.
 //
 // stream_read: every workgroup reads one contiguous 32 KB chunk, 256 threads x
 // 8 loads of 16 bytes, lane-contiguous (each load instruction covers 4 KB), all
@@ -105,7 +106,36 @@ __global__ void __launch_bounds__(kThreads) pull_dma(const unsigned char* src, u
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
+// The shader clock: one wave reads the shader-cycle counter (s_memtime) and
+// the constant 100 MHz counter (s_memrealtime), spins until the latter has
+// advanced `ticks` (or `max_iters` rounds have passed, so the wave always
+// ends), reads both again and stores the four values; the clock in MHz is
+// 100 * (cycles after - cycles before) / (ticks after - ticks before).
+__global__ void __launch_bounds__(64) sclk_probe(unsigned long long* out, unsigned ticks, unsigned max_iters) {
+    const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long r1 = r0;
+    for (unsigned i = 0; i < max_iters && r1 - r0 < ticks; ++i) r1 = __builtin_amdgcn_s_memrealtime();
+    const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+    r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[0] = c0;
+        out[1] = r0;
+        out[2] = c1;
+        out[3] = r1;
+    }
+}
+
 }  // namespace
+
+// One shader-clock reading on `stream` into out[0..3] (device memory, 32
+// bytes): cycles and 100 MHz ticks before and after a spin of `ticks` ticks
+// (1..100000).  Returns 0, or -1 for bad arguments or a failed launch.
+extern "C" int clove_diag_sclk(unsigned long long* out, unsigned ticks, void* stream) {
+    if (out == nullptr || ticks == 0 || ticks > 100000) return -1;
+    hipLaunchKernelGGL(sclk_probe, dim3(1), dim3(64), 0, (hipStream_t)stream, out, ticks, 1000000u);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // Reads `bytes` (a multiple of 16, 16-byte aligned) at src on `stream`.
 // Returns the number of workgroups launched, or -1 for bad arguments.
