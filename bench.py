@@ -602,6 +602,35 @@ def extras(compare_lib=False):
         record(f"fp16_llama1b_mlp_unfused_T{T}", calls, outs, flops,
                wb + 2 * 2 * T * H + 3 * 2 * 2 * T * I, PEAK_FP16_TFLOPS, check=chk_mlp(pairs[0], outs[0]))
         del pairs, outs, calls
+
+    # ---- large prefill MLP (T = 2048, hidden 4096, intermediate 11008): where
+    # gemm_fp16 takes its 256x256 tile, swiglu_fused runs the two GEMMs and
+    # swiglu; fused and unfused side by side ----
+    T, H, I = 2048, 4096, 11008
+    x = f16((T, H), 1.0, 970)
+    w = (f16((H, I), 0.02, 971), f16((H, I), 0.02, 972))
+    o = torch.empty(T, I, dtype=torch.float16, device="cuda")
+    gate = torch.empty(T, I, dtype=torch.float16, device="cuda")
+    up = torch.empty_like(gate)
+    flops = 2 * 2 * T * H * I
+    nb = 2 * H * I * 2 + 2 * T * H + 2 * T * I
+
+    def chk_big():
+        rows = pick_rows(T)
+        xr = host(x)[rows]
+        g_ = oracle.gemm_fp16_f64(xr, host(w[0])).astype(np.float16)
+        u_ = oracle.gemm_fp16_f64(xr, host(w[1])).astype(np.float16)
+        return tol(host(o)[rows], oracle.swiglu(g_, u_).astype(np.float64))
+    record("fp16_mlp_swiglu_fused_2048x4096x11008", [lambda: cg.swiglu_fused(x, w[0], w[1], o, T, H, I)] * 4,
+           [o], flops, nb, PEAK_FP16_TFLOPS, replays=3, check=chk_big)
+
+    def unfused_big():
+        cg.gemm_fp16(x, w[0], gate, T, I, H)
+        cg.gemm_fp16(x, w[1], up, T, I, H)
+        cg.swiglu(gate, up, o, T * I)
+    record("fp16_mlp_unfused_2048x4096x11008", [unfused_big] * 4, [o], flops, nb + 3 * 2 * 2 * T * I,
+           PEAK_FP16_TFLOPS, replays=3, check=chk_big)
+    del x, w, o, gate, up
     return out
 
 

@@ -306,10 +306,13 @@ clove_status_t clove_gemm_fp16(const void* A, const void* B, void* C, int M, int
 clove_status_t clove_gemm_fp16_noalloc(const void* A, const void* B, void* C, int M, int N, int K,
                                        float alpha, float beta, void* stream) {
     if (t_ws.mode == WsMode::kQuery) {
-        // plan and validate as clove_gemm_fp16; the fixed array is not the
+        // plan and validate as clove_gemm_fp16, and report a call the fixed
+        // array cannot hold as the real call would; the array is not the
         // caller's workspace, so the query's size is left as it was
         const size_t need = t_ws.need;
-        const clove_status_t st = clove_gemm_fp16(A, B, C, M, N, K, alpha, beta, stream);
+        t_ws.need = 0;
+        clove_status_t st = clove_gemm_fp16(A, B, C, M, N, K, alpha, beta, stream);
+        if (st == CLOVE_OK && t_ws.need > kNoAllocBytes) st = CLOVE_ERR_SCRATCH_LIMIT;
         t_ws.need = need;
         return st;
     }

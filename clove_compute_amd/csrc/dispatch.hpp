@@ -151,6 +151,9 @@ bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t
 // the same for T <= 4 on the FP16 GEMV (gemm_fp16.hip): each workgroup streams
 // 128 columns of W_gate and the same 128 columns of W_up; false when the
 // operands are not 16-byte aligned or hidden / inter are not multiples of 8
+// true when launch_gemm_fp16 runs one (unbatched) M x N x K product on the
+// 256x256 LDS-DMA tile (dma::gemm_f16_big)
+bool fp16_takes_big_tile(const void* A, const void* B, const void* C, int M, int N, int K, int cus);
 bool try_gemv_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* W_up, uint16_t* out, int T,
                      int hidden, int inter, hipStream_t stream, clove_status_t* status);
 

@@ -301,6 +301,11 @@ bool try_gemv_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t* 
     return true;
 }
 
+bool fp16_takes_big_tile(const void* A, const void* B, const void* C, int M, int N, int K, int cus) {
+    using namespace fp16;
+    return M > 4 && (int64_t)cdiv(M, 256) * cdiv(N, 256) >= cus / 2 && dma_eligible(A, B, C, M, N, K);
+}
+
 clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch,
                                 int M, int N, int K, float alpha, float beta,
                                 hipStream_t stream) {

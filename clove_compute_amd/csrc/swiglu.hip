@@ -12,7 +12,9 @@
 //    MFMA kernel with two B operands for T > 4 and for T = 2..4 on large
 //    weights, as gemm_fp16 decides per projection (both bit-identical to two
 //    gemm_fp16 calls followed by swiglu on the shapes where gemm_fp16 takes
-//    the same kernel family), and for shapes outside both (unaligned
+//    the same kernel family); where gemm_fp16 takes its 256x256 tile (large
+//    prefill) exactly those two calls and swiglu, with the up projection in a
+//    library buffer; and for shapes outside all of these (unaligned
 //    operands, hidden % 64 != 0 at T > 4) swiglu_fused_direct: one thread per
 //    output column and up to four tokens, fp32 fmaf over k in order -- the
 //    arithmetic of the reference's naive kernel (src/kernels/gemm_fp16.cu:
@@ -106,6 +108,18 @@ clove_status_t launch_swiglu_fused_fp16(const uint16_t* X, const uint16_t* W_gat
     DeviceInfo dev;
     clove_status_t st = current_device_info(&dev);
     if (st != CLOVE_OK) return st;
+    // where gemm_fp16 takes the 256x256 tile for the projections (large
+    // prefill), the same two calls and SwiGLU: gate into out, up into a
+    // library buffer, SwiGLU in place -- the two-GEMM result by construction
+    if (fp16_takes_big_tile(X, W_gate, out, T, inter, hidden, dev.num_cus) &&
+        fp16_takes_big_tile(X, W_up, out, T, inter, hidden, dev.num_cus)) {
+        void* ubuf = nullptr;
+        if ((st = acquire_buffer(stream, kBufSwiglu, (size_t)T * inter * 2, &ubuf)) != CLOVE_OK) return st;
+        uint16_t* up = static_cast<uint16_t*>(ubuf);
+        if ((st = launch_gemm_fp16(X, W_gate, out, 1, T, inter, hidden, 1.0f, 0.0f, stream)) != CLOVE_OK) return st;
+        if ((st = launch_gemm_fp16(X, W_up, up, 1, T, inter, hidden, 1.0f, 0.0f, stream)) != CLOVE_OK) return st;
+        return launch_swiglu(out, up, out, (int64_t)T * inter, stream);
+    }
     // (the kernel family gemm_fp16 takes for each projection: the skinny
     // kernel first where it would, then the GEMV for T <= 4)
     if (skinny_before_gemv(T, inter, hidden) &&

@@ -212,11 +212,18 @@ clove_status_t clove_swiglu(const void* gate, const void* up, void* output, int 
  * input [batch_seq, hidden_dim], W_gate / W_up [hidden_dim, intermediate_dim]
  * (gemm_fp16's B layout), output [batch_seq, intermediate_dim], all fp16.
  * Replaces clove::swiglu_fused, declared in include/clove/kernels/
- * activations.cuh:37-46 and never defined there.  One launch that writes
- * neither projection to memory: each output tile's gate and up sums are
- * formed side by side (the same k order as two separate gemm_fp16 calls, so
- * the result equals gemm_fp16 x 2 followed by clove_swiglu bit for bit) and
- * the epilogue applies SwiGLU to their fp16 values.
+ * activations.cuh:37-46 and never defined there.  Where gemm_fp16 would run
+ * each projection on its GEMV or skinny MFMA kernel (aligned operands, the
+ * decode and small-batch shapes), one launch that writes neither projection
+ * to memory: each output tile's gate and up sums are formed side by side in
+ * the k order of those kernels, so the result equals gemm_fp16 x 2 followed
+ * by clove_swiglu bit for bit, and the epilogue applies SwiGLU to their fp16
+ * values.  Where gemm_fp16 takes its 256x256 tile (large prefill), exactly
+ * those two calls and clove_swiglu, the up projection in a library buffer of
+ * batch_seq x intermediate_dim fp16 (bit-identical by construction).  Other
+ * shapes (unaligned operands, or hidden_dim % 64 != 0 beyond 4 rows): one
+ * direct kernel with the reference naive kernel's fp32 k-order arithmetic for
+ * both projections, within the FP16 tolerance of the two-call result.
  */
 clove_status_t clove_swiglu_fused(const void* input, const void* W_gate, const void* W_up,
                                   void* output, int batch_seq, int hidden_dim,
@@ -277,7 +284,10 @@ size_t clove_workspace_query_end(void);
  * (M, N >= 2048) that split nothing.  The first call on a device clears the array's counters
  * with one small kernel on `stream`.  Every call on a GPU shares that GPU's
  * array: calls that may overlap on one GPU (other streams, other host
- * threads) race and must be serialised by the caller.
+ * threads) race and must be serialised by the caller.  Inside a workspace
+ * size query it validates and plans as clove_gemm_fp16, returns
+ * CLOVE_ERR_SCRATCH_LIMIT for a call the array cannot hold, and leaves the
+ * query's size as it was (the array is not the caller's workspace).
  */
 #define CLOVE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 clove_status_t clove_gemm_fp16_noalloc(const void* A, const void* B, void* C,

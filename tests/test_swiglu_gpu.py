@@ -230,12 +230,15 @@ def test_swiglu_fused_fp16(T, H, I):
 
 @pytest.mark.parametrize("T,H,I", [(1, 2048, 8192), (2, 1024, 512), (4, 4096, 264), (7, 64, 96),
                                    (40, 1024, 520), (64, 512, 1000), (128, 4096, 1024), (300, 512, 768),
-                                   (512, 2048, 8192), (3, 4096, 4096), (2, 4096, 11008)])
+                                   (512, 2048, 8192), (3, 4096, 4096), (2, 4096, 11008),
+                                   (1024, 2048, 8192), (2048, 4096, 11008)])
 def test_swiglu_fused_equals_gemms_then_swiglu(T, H, I):
     # the fused kernels sum gate and up in the order gemm_fp16 does for the
     # same shape (same kernel family, tiles and split plan: the GEMV, or the
     # skinny kernel for T > 4 and for T = 2..4 on large weights), so the result
-    # is the two GEMMs followed by swiglu, bit for bit
+    # is the two GEMMs followed by swiglu, bit for bit; where gemm_fp16 takes
+    # its 256x256 tile (1024 x 2048 x 8192 and 2048 x 4096 x 11008: the tiles of
+    # [T, I] cover half the CUs) the fused call is those two GEMMs and swiglu
     X, Wg, Wu, _ = make_mlp(T, H, I, "bits")
     got = run_swiglu_fused(X, Wg, Wu)
     cg = _cg()

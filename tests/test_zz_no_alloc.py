@@ -5,8 +5,10 @@ The two run the same kernels with the same split plans, so their outputs are
 compared bit for bit: two calls in a row (the second smaller, reusing the
 fixed array and its re-armed counters), then the first shape again.  A call
 whose split-K scratch exceeds CLOVE_NOALLOC_SCRATCH_BYTES is rejected before
-anything is launched, and the documented domain (M <= 512, N, K <= 8192,
-aligned, N % 8 == 0, K % 64 == 0) is checked with the library's own size query.
+anything is launched (and a size query reports it the same way), the
+documented domain (M <= 512, N, K <= 8192, aligned, N % 8 == 0, K % 64 == 0)
+is checked with the library's own size query, and a first call on a fresh
+stream is captured into a HIP graph and replayed against the eager output.
 """
 import ctypes
 
@@ -96,3 +98,62 @@ def test_noalloc_documented_domain_fits():
     assert 0 < worst <= cg.CLOVE_NOALLOC_SCRATCH_BYTES, worst
     big = torch.empty(4096, 4096, dtype=torch.float16, device="cuda")
     assert _query_need(4096, 4096, 4096, big, big.clone(), big.clone()) == 0
+
+
+def test_noalloc_in_a_size_query():
+    # inside a query the entry point plans like the real call: a call beyond
+    # the array is reported as CLOVE_ERR_SCRATCH_LIMIT, one that fits as OK,
+    # and the query's size is not changed by either
+    import torch
+    import clove_compute_amd as cg
+    from clove_compute_amd import _lib
+    L = _lib.lib()
+    A = empty_f16(4, 32768)
+    B = torch.zeros(32768, 32768, dtype=torch.float16, device="cuda")
+    C = empty_f16(4, 32768, fill=float("nan"))
+    A2, B2, C2 = empty_f16(128, 4096), empty_f16(4096, 4096), empty_f16(128, 4096)
+    assert L.clove_workspace_query_begin() == 0
+    big = _abi("clove_gemm_fp16_noalloc", A, B, C, 4, 32768, 32768)
+    fits = _abi("clove_gemm_fp16_noalloc", A2, B2, C2, 128, 4096, 4096)
+    need = L.clove_workspace_query_end()
+    assert big == cg.CLOVE_ERR_SCRATCH_LIMIT
+    assert fits == 0
+    assert need == 0
+    torch.cuda.synchronize()
+    assert np.all(np.isnan(to_host(C).astype(np.float32)))  # a query launches nothing
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 4096, 4096), (2, 1024, 2048)])
+def test_noalloc_first_call_on_a_fresh_stream_captured(M, N, K):
+    # the split-K skinny kernel and the split-K GEMV: the first call on a new
+    # stream is captured into a HIP graph (nothing to allocate), replayed three
+    # times with eager work and synchronisation between the replays, and every
+    # replay's output equals the eager call's bit for bit
+    import torch
+    g = rng("noalloc-graph", M, N, K)
+    A = to_dev(g.standard_normal((M, K)).astype(np.float16))
+    B = to_dev((g.standard_normal((K, N)) * 0.05).astype(np.float16))
+    C_eager = empty_f16(M, N)
+    assert _abi("clove_gemm_fp16_noalloc", A, B, C_eager, M, N, K) == 0
+    torch.cuda.synchronize()
+    ref = to_host(C_eager)
+    C = empty_f16(M, N)
+    # operands of the eager call made between the replays (64 x 512 x 1024)
+    X2 = torch.ones(64, 1024, dtype=torch.float16, device="cuda")
+    W2 = torch.full((1024, 512), 0.5, dtype=torch.float16, device="cuda")
+    O2 = empty_f16(64, 512)
+    s = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        st = _abi("clove_gemm_fp16_noalloc", A, B, C, M, N, K)
+    assert st == 0
+    for i in range(3):
+        C.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(f16bits(to_host(C)), f16bits(ref)), i
+        # eager work between replays, on the same array
+        assert _abi("clove_gemm_fp16_noalloc", X2, W2, O2, 64, 512, 1024) == 0
+        torch.cuda.synchronize()
+        assert torch.all(O2 == 512.0)
+    del graph
