@@ -32,17 +32,27 @@
 // its zero point) and the Bt fragment "B", so a lane's outputs are one column
 // 32 b + m per block and 16 rows.  In k-step s of a group, lane half h holds
 // k = 64 h + 16 s .. +15 of both operands.  The unpack lane also turns its
-// row's fp16 scale into fp32 (NaN for a bad zero point) and passes it to the
-// lanes that fold that row through a per-wave LDS slot.  The int32 sums are
-// double-buffered: a group's MFMAs run interleaved with the fold of the
-// wave's previous group, so the fold (VALU) overlaps the matrix core.
+// row's fp16 scale into fp32 (NaN for a bad zero point); with the lane's
+// column scale sB it forms the group's scale products sA[row] * sB[col] for
+// all the wave's outputs as one v_mfma_f32_32x32x2_f32 outer product per
+// column block (the unpack lane is the A operand's row, the column lane the B
+// operand's column; k = 1 carries zeros), which lands in the accumulator
+// layout: the fold is then 2 VALU per output (convert, fma) and no scale
+// crosses lanes.  The int32 sums and scale products are double-buffered: a
+// group's MFMAs run interleaved with the fold of the wave's previous group,
+// so the fold (VALU) overlaps the matrix core.
 //
 // Streams.  The weight rows come from HBM, Bt from L2.  Vector-memory
 // completions count in issue order per wave, so the two streams are issued
-// by different waves: set 0 issues the weight pieces (and zA / sA) LA - 1
-// stages ahead from an LA-deep ring, set 1 the Bt pieces (and sBf) two
-// stages ahead from a three-deep ring, and each wave waits only for its own
-// stream before the workgroup barrier that publishes a stage.
+// by different waves: set 0 issues the weight pieces (and zA / sA), set 1 the
+// Bt pieces (and sBf), each LA - 1 (LB - 1) stages ahead from an LA (LB) deep
+// ring, and each wave waits only for its own stream before the workgroup
+// barrier that publishes a stage.  One stage ahead is enough: a stage's loads
+// land within the stage of compute they overlap (~1.5 us), and deeper rings
+// only make every workgroup's first stage wait behind the whole chip's
+// initial burst (per-workgroup timestamps at 4096x11008 N = 128: first stage
+// after 6.1 us with 5 + 2 stages in flight, after 2.6 us with 1 + 1; the
+// steady-state stage time the same).
 //
 // Partials mode (PART, the group-partials test hook): each wave stores its
 // group's int32 sums P_g to P [M, N, G] instead of folding them (INT32_MIN
@@ -95,14 +105,13 @@ struct Args {
 constexpr int NW = 8, NT = 512;
 constexpr int BR = 64, BC = 128;
 constexpr int NB = 2;          // 32x32 blocks per wave: 32 rows x 64 columns
-constexpr int LA = 6, LB = 3;  // weight / Bt stages in the rings
+constexpr int LA = 2, LB = 2;  // weight / Bt stages in the rings (one stage ahead, see the header)
 constexpr int DA = 3, DB = 9;  // DMAs per stage of a weight wave / of a Bt wave
 constexpr int ZA_OFF = BR * 128, SA_OFF = ZA_OFF + BR * 4, AST = SA_OFF + BR * 4;
 constexpr int SB_OFF = 2 * BC * 128, BST = SB_OFF + 2 * BC * 4;
 constexpr int BT0 = LA * AST;
 constexpr int JUNK = BT0 + LB * BST;  // dummy DMA target, 1 KB
-constexpr int XS_OFF = JUNK + 1024;   // per-wave row-scale slots, 32 fp32 each
-constexpr int LDS = XS_OFF + NW * 128;
+constexpr int LDS = JUNK + 1024;
 constexpr int PREP_COLS = 64;         // i4_prep_bt columns per workgroup
 static_assert(AST % 256 == 0 && BST % 256 == 0, "stage alignment");
 static_assert(BR / 8 == 2 * 4 && 2 * BC * 128 / 1024 == 8 * 4, "DMA blocks per wave");
@@ -339,7 +348,6 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
     const int ncol0 = 64 * cw;
     const unsigned bbase = set * (BC * 128);
     const unsigned sbase = SB_OFF + set * (BC * 4) + 4 * (ncol0 + m);
-    const unsigned xs = lds0 + XS_OFF + wave * 128;
     const int half = 16 * set;  // the fp16 half of a (g, g+1) dword that is this wave's group
 
     f32x16 facc[NB];
@@ -350,8 +358,8 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
 
     // one group: wait for its stage, refill the ring, MFMAs into `cur` with
     // the fold of `prev` (the previous group's sums and scales) interleaved
-    auto step = [&](int t, i32x16 (&cur)[NB], u32x4 (&scur)[4], float (&bcur)[NB], const i32x16 (&prev)[NB],
-                    const u32x4 (&sprev)[4], const float (&bprev)[NB]) {
+    auto step = [&](int t, i32x16 (&cur)[NB], f32x16 (&spc)[NB], const i32x16 (&prev)[NB],
+                    const f32x16 (&spp)[NB]) {
         const int rem = nst - 1 - t;
         if (set == 0) wait_stages<DA>(min(rem, LA - 2));
         else wait_stages<DB>(min(rem, LB - 2));
@@ -368,9 +376,10 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
         const unsigned zw = ld4(sa_st + ZA_OFF + 4 * rA);
         const unsigned sw = ld4(sa_st + SA_OFF + 4 * rA);
         const u32x4 p0 = ld16(sa_st + aoff0), p1 = ld16(sa_st + aoff1);
+        float bcol[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-            bcur[b] = *reinterpret_cast<const lds_f32*>((size_t)(sb_st + sbase + 4 * 32 * b));
+            bcol[b] = *reinterpret_cast<const lds_f32*>((size_t)(sb_st + sbase + 4 * 32 * b));
         i32x4 bf[NB][4];
 #pragma unroll
         for (int s = 0; s < 2; ++s)
@@ -381,13 +390,14 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
             }
         __builtin_amdgcn_sched_barrier(0);
 
-        // ---- the unpack row: its scale (NaN for a bad zero point) to the
-        // wave's slot, its weights as int8 q - z ----
+        // ---- the unpack row: its weights as int8 q - z, and its scale (NaN
+        // for a bad zero point); the scale products of the group's outputs
+        // sA[row] * sB[col] as one 32x32x2 fp32 MFMA outer product per column
+        // block (k = 0 carries the scales, k = 1 zeros), in the accumulator
+        // layout, so the fold needs no row-scale exchange between lanes ----
         int z;
         const bool zok = zero_ok((uint16_t)(zw >> half), z);
         const float sa_row = zok ? (PART ? 0.0f : h2f((uint16_t)(sw >> half))) : __builtin_nanf("");
-        // (both lane halves hold the row: the same value to the same slot)
-        *reinterpret_cast<lds_f32*>((size_t)(xs + 4 * m)) = sa_row;
         const unsigned zp = (unsigned)(128 - z) * 0x01010101u;
         i32x4 wq[4];
         {
@@ -399,18 +409,19 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
                 wq[d >> 1][2 * (d & 1) + 1] = (int)((lo + zp) ^ 0x80808080u);
             }
         }
-        // the scales of this lane's 16 output rows 8 j + 4 h + e (same wave:
-        // LDS returns the slot's new value)
+        const float sa_op = h == 0 ? sa_row : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) scur[j] = ld16(xs + 4 * (8 * j + 4 * h));
+        for (int b = 0; b < NB; ++b)
+            spc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(sa_op, h == 0 ? bcol[b] : 0.0f, f32x16{}, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
 
         // ---- NB x 4 MFMAs (k-step s of the column blocks; the next two
         // steps' Bt fragments read meanwhile) with the previous group's fold
-        // (3 VALU per output: 12 per MFMA) placed between them.  The empty asm
-        // statements fence the fold into this region: its inputs are defined
-        // at the start, its results used at the end (otherwise the compiler
-        // sinks it to the next group's block, in series with those MFMAs) ----
+        // (2 VALU per output: convert, fma; 8 per MFMA) placed between them.
+        // The empty asm statements fence the fold into this region: its
+        // inputs are defined at the start, its results used at the end
+        // (otherwise the compiler sinks it to the next group's block, in
+        // series with those MFMAs) ----
         if constexpr (PART) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
@@ -428,7 +439,8 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
                                                                    0, 0, 0);
             }
             // P[row][col][g]; a NaN row scale (the unpack lane's bad zero
-            // point) or column scale (i4_prep_bt's) marks the sum invalid
+            // point) or column scale (i4_prep_bt's) makes the product NaN and
+            // marks the sum invalid
             const int g = gbeg + 2 * t + set;
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -436,7 +448,7 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int row = m0 + 32 * rw + 8 * (i >> 2) + 4 * h + (i & 3);
-                    const float chk = bitcast<float>(scur[i >> 2][i & 3]) + bcur[b];
+                    const float chk = spc[b][i];
                     if (row < M && col < p.N)
                         p.P[((int64_t)row * p.N + col) * G + g] = chk == chk ? cur[b][i] : (int)0x80000000u;
                 }
@@ -444,12 +456,13 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
             return;
         }
         i32x16 pv[NB];
-        f32x16 fa[NB];
+        f32x16 fa[NB], sp[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             pv[b] = prev[b];
             fa[b] = facc[b];
-            asm volatile("" : "+v"(pv[b]), "+v"(fa[b]));
+            sp[b] = spp[b];
+            asm volatile("" : "+v"(pv[b]), "+v"(fa[b]), "+v"(sp[b]));
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
@@ -469,15 +482,14 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                fa[b][i] = fmaf(bitcast<float>(sprev[i >> 2][i & 3]) * bprev[b], (float)pv[b][i], fa[b][i]);
+            for (int i = 0; i < 16; ++i) fa[b][i] = fmaf(sp[b][i], (float)pv[b][i], fa[b][i]);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             if (s < 2) __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);  // DS reads
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
             }
         }
 #pragma unroll
@@ -499,36 +511,32 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
             if (t < nst) issue_b(t);
     }
 
-    // two sets of sums and scales, alternating (no copies between steps); the
-    // first fold reads zeros
+    // two sets of sums and scale products, alternating (no copies between
+    // steps); the first fold reads zeros
     i32x16 ix[NB], iy[NB];
-    u32x4 sx[4], sy[4];
-    float bx[NB], by[NB];
+    f32x16 px[NB], py[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         iy[b] = i32x16{};
-        by[b] = 0.0f;
+        py[b] = f32x16{};
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sy[j] = u32x4{0u, 0u, 0u, 0u};
     int t = 0;
     for (; t + 1 < nst; t += 2) {
-        step(t, ix, sx, bx, iy, sy, by);
-        step(t + 1, iy, sy, by, ix, sx, bx);
+        step(t, ix, px, iy, py);
+        step(t + 1, iy, py, ix, px);
     }
     // the last group's fold
-    auto fold = [&](const i32x16 (&c)[NB], const u32x4 (&sc)[4], const float (&bc)[NB]) {
+    auto fold = [&](const i32x16 (&c)[NB], const f32x16 (&sp)[NB]) {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                facc[b][i] = fmaf(bitcast<float>(sc[i >> 2][i & 3]) * bc[b], (float)c[b][i], facc[b][i]);
+            for (int i = 0; i < 16; ++i) facc[b][i] = fmaf(sp[b][i], (float)c[b][i], facc[b][i]);
     };
     if (t < nst) {
-        step(t, ix, sx, bx, iy, sy, by);
-        fold(ix, sx, bx);
+        step(t, ix, px, iy, py);
+        fold(ix, px);
     } else {
-        fold(iy, sy, by);
+        fold(iy, py);
     }
     // every DMA has landed and every wave is done with the stages
     dma::stage_barrier<vmcnt_imm(0)>();

@@ -11,8 +11,7 @@ DMA offsets and checks:
     against each other and the LDS size;
   * the ring: the slot a stage is issued into is not the one being read,
     and each wave's vmcnt wait leaves exactly the later stages in flight;
-  * the row-scale slots, the partials (P) store index and the epilogue
-    staging bounds.
+  * the partials (P) store index and the epilogue staging bounds.
 Constants are read from the kernel header so the replay follows the source.
 """
 import os
@@ -41,14 +40,12 @@ def _consts():
     c["BST"] = c["SB_OFF"] + 2 * c["BC"] * 4
     c["BT0"] = c["LA"] * c["AST"]
     c["JUNK"] = c["BT0"] + c["LB"] * c["BST"]
-    c["XS_OFF"] = c["JUNK"] + 1024
-    c["LDS"] = c["XS_OFF"] + c["NW"] * 128
+    c["LDS"] = c["JUNK"] + 1024
     # the header's own derivations must match the ones above
     for expr, key in [(r"ZA_OFF = BR \* 128", "ZA_OFF"), (r"SA_OFF = ZA_OFF \+ BR \* 4", "SA_OFF"),
                       (r"AST = SA_OFF \+ BR \* 4", "AST"), (r"SB_OFF = 2 \* BC \* 128", "SB_OFF"),
                       (r"BST = SB_OFF \+ 2 \* BC \* 4", "BST"), (r"BT0 = LA \* AST", "BT0"),
-                      (r"JUNK = BT0 \+ LB \* BST", "JUNK"), (r"XS_OFF = JUNK \+ 1024", "XS_OFF"),
-                      (r"LDS = XS_OFF \+ NW \* 128", "LDS")]:
+                      (r"JUNK = BT0 \+ LB \* BST", "JUNK"), (r"LDS = JUNK \+ 1024", "LDS")]:
         assert re.search(expr, src), key
     return c
 
@@ -95,8 +92,7 @@ def replay(M, N, K, part):
     n_a, n_za, n_bt, n_sb = M * KB, M * G * 2, G * Npad * 128, G * Npad * 4
     lane = np.arange(64)
     # LDS regions: [weight stages][Bt stages][junk][row-scale slots]
-    regions = {"a": (0, C["BT0"]), "b": (C["BT0"], C["JUNK"]), "junk": (C["JUNK"], C["XS_OFF"]),
-               "xs": (C["XS_OFF"], C["LDS"])}
+    regions = {"a": (0, C["BT0"]), "b": (C["BT0"], C["JUNK"]), "junk": (C["JUNK"], C["LDS"])}
     assert C["LDS"] <= 160 * 1024
     rows_loaded = {}
     for split in range(nsplit):
@@ -179,10 +175,6 @@ def replay(M, N, K, part):
                 for r in range(m0, min(M, m0 + BR)):
                     for c in range(8):
                         assert (split, tile, t, r, c) in rows_loaded
-    # row-scale slots: lane m writes 4 m, lanes read 16 bytes at 4 (8 j + 4 h)
-    m = np.arange(32)
-    assert (4 * m + 4).max() <= 128
-    assert max(4 * (8 * j + 4 * h) + 16 for j in range(4) for h in range(2)) <= 128
     # epilogue staging (fp16 tile, pitch BC + 8 halves) and the set-1 hand-off
     assert BR * (BC + 8) * 2 <= C["BT0"] + C["LB"] * C["BST"]
     assert 4 * 64 * NB * 16 * 4 <= C["BT0"] + C["LB"] * C["BST"]
