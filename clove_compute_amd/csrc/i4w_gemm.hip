@@ -12,7 +12,12 @@ using namespace i4w;
 // (WR, WC, FW, FX, stages): waves along weight rows x along X rows, 32x32
 // tiles per wave in each direction
 using CfgBig = Cfg<4, 1, 2, 4, 3>;  // 256 x 128, 4 waves of 64 x 128
-using CfgC64 = Cfg<4, 1, 1, 2, 3>;  // 128 x 64 (75 KB LDS: two workgroups per CU)
+// 128 x 64, one stage ahead (50 KB LDS: two workgroups per CU).  The
+// prefill GEMMs are bound by the VALU and MFMA issue, not by their loads: a
+// second stage in flight only made every workgroup's first stage wait behind
+// a larger burst of the grid's prologue loads (W4A16 Llama-1B layer T = 512
+// 125.6 -> 122.9 us, fused 114.9 -> 111.1 us against three stages)
+using CfgC64 = Cfg<4, 1, 1, 2, 2>;
 using CfgC32 = Cfg<2, 1, 1, 1, 4>;  // 64 x 32, 2 waves (several workgroups per CU)
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
