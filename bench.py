@@ -664,6 +664,24 @@ def floor():
                      "GBs_cold": round(nbytes / us / 1e3, 1), "us_hot": round(hot, 3),
                      "GBs_hot": round(nbytes / hot / 1e3, 1)}
         print(f"[floor] {name}: cold {us:.2f} us, hot {hot:.2f} us", file=sys.stderr, flush=True)
+        # the second design: persistent workgroups over contiguous slices
+        lib.clove_diag_stream_read_persistent.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        lib.clove_diag_stream_read_persistent.restype = ctypes.c_int
+        for grid, depth in ((256, 4), (256, 8), (512, 4), (512, 8)):
+            def pcall(b, grid=grid, depth=depth):
+                stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+                if lib.clove_diag_stream_read_persistent(b.data_ptr(), nbytes, grid, depth, sink.data_ptr(),
+                                                         stream) != grid:
+                    raise RuntimeError("clove_diag_stream_read_persistent failed")
+            pcalls = [lambda b=b: pcall(b) for b in bufs]
+            pus = graph_time(pcalls, [], 5)
+            phot = graph_time(pcalls[:1] * 16, [], 5)
+            out[f"{name}_persistent_{grid}x1024_{16 * depth}KB"] = {
+                "us_cold": round(pus, 3), "GBs_cold": round(nbytes / pus / 1e3, 1), "us_hot": round(phot, 3),
+                "GBs_hot": round(nbytes / phot / 1e3, 1)}
+            print(f"[floor] {name} persistent {grid} x 1024, {16 * depth} KB in flight: cold {pus:.2f} us, "
+                  f"hot {phot:.2f} us", file=sys.stderr, flush=True)
         del bufs, calls
     # one CU's pull rate: 32 workgroups, each streaming 1 MB of a 32 MB buffer
     # (at most one workgroup per CU) with 32 KB or 128 KB in flight, cold and hot

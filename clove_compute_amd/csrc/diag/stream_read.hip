@@ -106,6 +106,31 @@ __global__ void __launch_bounds__(kThreads) pull_dma(const unsigned char* src, u
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
+// A second floor design: a persistent grid of `gridDim.x` workgroups of 1024
+// threads, workgroup b streaming the b-th contiguous slice of the buffer in
+// steps of 16 KB (one 16-byte load per thread), D steps in flight per thread
+// (D x 16 KB per workgroup), lane-contiguous like the one-shot kernel.  Loads
+// past the end read the last element (clamped, unconditional).
+template <int D>
+__global__ void __launch_bounds__(1024) stream_read_persistent(const u32x4* src, size_t n16, size_t per16,
+                                                               unsigned* sink) {
+    const size_t base = (size_t)blockIdx.x * per16 + threadIdx.x;
+    const size_t nsteps = per16 / 1024;
+    auto ld = [&](size_t s) { return __builtin_nontemporal_load(src + min(base + s * 1024, n16 - 1)); };
+    u32x4 v[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) v[d] = ld(d);
+    unsigned x = 0;
+    for (size_t s = 0; s < nsteps; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            x ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+            if (s + d + D < nsteps) v[d] = ld(s + d + D);
+        }
+    }
+    if (x == 0x9e3779b9u && threadIdx.x == 0) sink[blockIdx.x & 1023] = x;
+}
+
 // The shader clock: one wave reads the shader-cycle counter (s_memtime) and
 // the constant 100 MHz counter (s_memrealtime), spins until the latter has
 // advanced `ticks` (or `max_iters` rounds have passed, so the wave always
@@ -135,6 +160,22 @@ extern "C" int clove_diag_sclk(unsigned long long* out, unsigned ticks, void* st
     if (out == nullptr || ticks == 0 || ticks > 100000) return -1;
     hipLaunchKernelGGL(sclk_probe, dim3(1), dim3(64), 0, (hipStream_t)stream, out, ticks, 1000000u);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// `bytes` (a multiple of 16, 16-byte aligned) read by `grid` persistent
+// workgroups (1..4096) of 1024 threads, each over one contiguous slice, with
+// `depth` (4 or 8) 16 KB steps in flight per workgroup.  Returns grid, or -1.
+extern "C" int clove_diag_stream_read_persistent(const void* src, size_t bytes, int grid, int depth,
+                                                 unsigned* sink, void* stream) {
+    if (src == nullptr || sink == nullptr || bytes == 0 || bytes % 16 != 0 || grid <= 0 || grid > 4096 ||
+        (depth != 4 && depth != 8) || (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+        return -1;
+    const size_t n16 = bytes / 16;
+    const size_t per16 = (n16 + (size_t)grid * 1024 - 1) / ((size_t)grid * 1024) * 1024;  // whole 16 KB steps
+    auto k = depth == 8 ? stream_read_persistent<8> : stream_read_persistent<4>;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(1024), 0, (hipStream_t)stream,
+                       reinterpret_cast<const u32x4*>(src), n16, per16, sink);
+    return hipGetLastError() == hipSuccess ? grid : -1;
 }
 
 // Reads `bytes` (a multiple of 16, 16-byte aligned) at src on `stream`.
