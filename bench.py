@@ -74,6 +74,10 @@ def parse():
     ap.add_argument("--floor", action="store_true",
                     help="only measure the cold HBM streaming-read floor (lib/libclove_diag.so) at the "
                          "weight sizes of the memory-bound shapes and print one JSON line")
+    ap.add_argument("--phases", action="store_true",
+                    help="only measure the headline kernel's phases (prologue, K loop, epilogue, the spread "
+                         "and gaps between launches) from per-workgroup timestamps (lib/libclove_diag.so) and "
+                         "print one JSON line")
     ap.add_argument("--compare-lib", action="store_true",
                     help="also time torch.matmul (hipBLASLt) on the headline operands, in blocks "
                          "alternating with clove_gemm_fp16, and report both")
@@ -197,6 +201,132 @@ def measure_sclk(h, steps, ticks=200):
         return None
     return {"median": round(mhz[len(mhz) // 2], 1), "min": round(mhz[0], 1), "max": round(mhz[-1], 1),
             "probes": len(mhz)}
+
+
+def phases(args, timer, rounds=3, series=300):
+    """The headline kernel phase by phase.  dma::gemm_f16_big_ts is the
+    product kernel's body with shader-cycle (s_memtime) and 100 MHz
+    (s_memrealtime) timestamps at its phase boundaries, one record per
+    workgroup (libclove_diag.so clove_diag_fp16_big_phases).
+      1. `series` timestamped launches back to back from this process's
+         first GEMM launch: per launch the K loop's clock, the span of its
+         workgroups and the gap to the next launch (the shader clock's
+         response to the sustained load, launch by launch);
+      2. blocks of `steps` back-to-back launches of the product call and of
+         the timestamped kernel, alternating `rounds` times (per-launch event
+         time of each: the cost of the timestamps);
+      3. from the last timestamped block, per workgroup: the time from entry
+         until its first K tile has landed, the first two K tiles, the shader
+         cycles per K tile and the clock over the remaining K tiles, and the
+         output stores; per launch, the spread of the workgroups' starts and
+         ends and the gap to the next launch."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import clove_compute_amd as cg
+    from tests._util import to_dev
+    lib = diag_lib()
+    lib.clove_diag_fp16_big_phases.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 3 + [ctypes.c_void_p] * 2
+    lib.clove_diag_fp16_big_phases.restype = ctypes.c_int
+    n = 4096
+    g = np.random.default_rng(20261201)  # the headline's operands
+    A = to_dev(g.standard_normal((n, n)).astype(np.float16))
+    B = to_dev((g.standard_normal((n, n)) * 0.02).astype(np.float16))
+    C = torch.empty(n, n, dtype=torch.float16, device="cuda")
+    ref = torch.empty_like(C)
+    grid, words = 256, 16
+    steps = args.steps
+    nts = max(series, steps)
+    ts = torch.zeros(nts, grid, words, dtype=torch.int64, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+
+    def product(i):
+        cg.gemm_fp16(A, B, C, n, n, n)
+
+    def stamped(i):
+        if lib.clove_diag_fp16_big_phases(A.data_ptr(), B.data_ptr(), C.data_ptr(), n, n, n,
+                                          ctypes.c_void_p(ts[i % nts].data_ptr()), stream) != grid:
+            raise RuntimeError("clove_diag_fp16_big_phases failed")
+
+    def records(count):
+        t = ts[:count].cpu().numpy().astype(np.int64)
+        if not (t[:, :, 10] == n // 64).all():
+            raise RuntimeError("a workgroup wrote no record")
+        return t[:, :, 0:10:2], t[:, :, 1:10:2].astype(np.float64) * 0.01, t[:, :, 12]  # cycles, us, XCC
+
+    # 1. the series from the first launch
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(series // 10 + 1)]
+    ev[0].record()
+    for i in range(series):
+        stamped(i)
+        if (i + 1) % 10 == 0:
+            ev[(i + 1) // 10].record()
+    torch.cuda.synchronize()
+    cyc, rt, _ = records(series)
+    lmhz = np.median((cyc[:, :, 3] - cyc[:, :, 2]) / (rt[:, :, 3] - rt[:, :, 2]), axis=1)
+    sgap = rt[1:, :, 0].min(1) - rt[:-1, :, 4].max(1)
+    ser = [{"launches": f"{10 * j}-{10 * j + 9}",
+            "us_per_launch": round(ev[j].elapsed_time(ev[j + 1]) * 100.0, 1),
+            "k_loop_sclk_mhz": round(float(np.median(lmhz[10 * j:10 * j + 10])), 0),
+            "span_us": round(float(np.median(rt[10 * j:10 * j + 10, :, 4].max(1) - rt[10 * j:10 * j + 10, :, 0].min(1))), 1),
+            "gap_us": round(float(np.median(sgap[10 * j:min(10 * j + 10, series - 1)])), 2)}
+           for j in range(series // 10)]
+    cg.gemm_fp16(A, B, ref, n, n, n)
+    torch.cuda.synchronize()
+    if not torch.equal(C.view(torch.int16), ref.view(torch.int16)):
+        raise RuntimeError("the timestamped kernel's output differs from clove_gemm_fp16's")
+
+    # 2. alternating blocks
+    prod_us, ts_us = [], []
+    for _ in range(rounds):
+        prod_us.append(timer.run(product, steps, args.warmup) * 1e3)
+        ts_us.append(timer.run(stamped, steps, args.warmup) * 1e3)
+    torch.cuda.synchronize()
+    if not torch.equal(C.view(torch.int16), ref.view(torch.int16)):
+        raise RuntimeError("the timestamped kernel's output differs from clove_gemm_fp16's")
+
+    # 3. the last timestamped block
+    cyc, rt, xcc = records(steps)
+
+    def pct(v):
+        v = np.asarray(v, dtype=np.float64).ravel()
+        return {"p10": round(float(np.percentile(v, 10)), 3), "median": round(float(np.median(v)), 3),
+                "p90": round(float(np.percentile(v, 90)), 3)}
+
+    loop_cyc = (cyc[:, :, 3] - cyc[:, :, 2]) / (n // 64 - 2)
+    loop_us = rt[:, :, 3] - rt[:, :, 2]
+    loop_mhz = (cyc[:, :, 3] - cyc[:, :, 2]) / loop_us
+    first_mhz = (cyc[:, :, 1] - cyc[:, :, 0]) / np.maximum(rt[:, :, 1] - rt[:, :, 0], 0.01)
+    starts, ends = rt[:, :, 0], rt[:, :, 4]
+    span = ends.max(1) - starts.min(1)
+    gap = starts.min(1)[1:] - ends.max(1)[:-1]
+    out = {
+        "workload": "fp16_gemm_4096x4096x4096", "launches": steps, "workgroups": grid,
+        "series_from_first_launch": ser,
+        "us_per_launch_event": {"product": [round(x, 2) for x in prod_us], "timestamped": [round(x, 2) for x in ts_us]},
+        "per_workgroup_us": {
+            "entry_to_first_tile_landed": pct(rt[:, :, 1] - rt[:, :, 0]),
+            "first_two_k_tiles": pct(rt[:, :, 2] - rt[:, :, 1]),
+            "k_tiles_3_to_64": pct(loop_us),
+            "epilogue_to_stores_done": pct(rt[:, :, 4] - rt[:, :, 3]),
+            "workgroup_total": pct(ends - starts),
+        },
+        "k_loop_cycles_per_tile": pct(loop_cyc),
+        "k_loop_sclk_mhz": pct(loop_mhz),
+        "prologue_sclk_mhz": pct(first_mhz),
+        "k_loop_sclk_mhz_by_xcc": {int(x): round(float(np.median(loop_mhz[xcc == x])), 1)
+                                   for x in np.unique(xcc)},
+        "per_launch_us": {"start_spread": pct(starts.max(1) - starts.min(1)),
+                          "end_spread": pct(ends.max(1) - ends.min(1)),
+                          "span_first_start_to_last_end": pct(span),
+                          "gap_to_next_launch": pct(gap) if gap.size else None},
+        "mfma_bound_cycles_per_tile": 2048,
+        "device": device_info(),
+    }
+    print(json.dumps({"phases": out}), flush=True)
 
 
 def compare_library(h, timer, steps, warmup, rounds=3):
@@ -742,6 +872,9 @@ def main():
     _lib.lib()  # fails loudly when the HIP library is not built
     if args.floor:
         floor()
+        return
+    if args.phases:
+        phases(args, Timer())
         return
 
     timer = Timer()

@@ -254,11 +254,28 @@ __device__ __forceinline__ void acc_fence(f32x4 (&acc)[64]) {
     }
 }
 
-// (a template so that every translation unit that includes this header can
-// see it without defining the kernel twice; launched as gemm_f16_big<Big>)
-template <class CF>
-__global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
+// Per-workgroup phase timestamps of the TS instantiation (one record of
+// kTsWords 64-bit words per workgroup, written by wave 0 at the end): shader
+// cycles (s_memtime) and the constant 100 MHz clock (s_memrealtime) at
+// entry, once the first K tile has landed, after the first two K tiles, after
+// the last K tile and once the output stores have completed; then the
+// workgroup's tile count, HW_ID and XCC_ID.
+constexpr int kTsWords = 16;
+enum TsSlot : int { kTsEntry = 0, kTsFirst = 2, kTsTwo = 4, kTsLoop = 6, kTsEnd = 8, kTsKT = 10, kTsHw = 11 };
+
+// The kernel body.  TS = false is the product kernel; TS = true (bench.py's
+// phase breakdown) adds the timestamps above and nothing else: the
+// s_memtime / s_memrealtime reads at the phase boundaries (whose results the
+// compiler waits for with the LDS reads in flight at that point) and one
+// store per workgroup after the output stores.
+template <class CF, bool TS>
+__device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) {
     using Big = CF;
+    unsigned long long tsv[10] = {};
+    if constexpr (TS) {
+        tsv[kTsEntry] = __builtin_amdgcn_s_memtime();
+        tsv[kTsEntry + 1] = __builtin_amdgcn_s_memrealtime();
+    }
     constexpr int BM = Big::BM, BN = Big::BN, BK = Big::BK, NW = Big::NW;
     constexpr int WTM = Big::WTM, WTN = Big::WTN, FM = Big::FM, FN = Big::FN;
     constexpr int A_BYTES = Big::A_BYTES, B_BYTES = Big::B_BYTES;
@@ -334,6 +351,10 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
 #pragma unroll
     for (int i = 0; i < Big::DMA_B; ++i) dma_b(k1, 1, i);
     stage_barrier<vmcnt_imm(Big::DMA_A + Big::DMA_B)>();
+    if constexpr (TS) {
+        tsv[kTsFirst] = __builtin_amdgcn_s_memtime();
+        tsv[kTsFirst + 1] = __builtin_amdgcn_s_memrealtime();
+    }
 #pragma unroll
     for (int x = 0; x < 8; ++x) {
         fa[0][x] = rd_a(0, 0, x);
@@ -383,6 +404,12 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
     int kt = 0;
 #pragma unroll 1
     for (; kt + 1 < KT; kt += 2) {
+        if constexpr (TS) {
+            if (kt == 2) {
+                tsv[kTsTwo] = __builtin_amdgcn_s_memtime();
+                tsv[kTsTwo + 1] = __builtin_amdgcn_s_memrealtime();
+            }
+        }
         tile(kt, IntC<0>{});
         tile(kt + 1, IntC<1>{});
     }
@@ -390,6 +417,29 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
     // every DMA has landed and every wave is done with the stages
     stage_barrier<vmcnt_imm(0)>();
     acc_fence<1>(acc);  // the last MFMA results land before the accumulators are read
+    if constexpr (TS) {
+        tsv[kTsLoop] = __builtin_amdgcn_s_memtime();
+        tsv[kTsLoop + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+    // TS: the end time once this wave's output stores have completed, and the record
+    auto ts_end = [&]() {
+        if constexpr (TS) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            tsv[kTsEnd] = __builtin_amdgcn_s_memtime();
+            tsv[kTsEnd + 1] = __builtin_amdgcn_s_memrealtime();
+            if (wave == 0 && lane == 0) {
+                unsigned hw, xcc;
+                asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+                asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+                unsigned long long* r = ts + (size_t)blockIdx.x * kTsWords;
+#pragma unroll
+                for (int i = 0; i < 10; ++i) r[i] = tsv[i];
+                r[kTsKT] = (unsigned long long)KT;
+                r[kTsHw] = hw;
+                r[kTsHw + 1] = xcc;
+            }
+        }
+    };
 
     uint16_t* C = p.C + batch * p.sC;
     const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
@@ -408,13 +458,18 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's writes are visible to its reads
         constexpr int CPRW = WTN / 8;          // 16-byte chunks per row of the wave tile
         constexpr int RPI = 64 / CPRW;         // rows per store instruction
+        // Nontemporal stores: C does not stay dirty in the XCDs' L2s, whose
+        // write-back at the end of the kernel otherwise delays the next
+        // launch (4096^3: 3.0 -> 1.4 us between back-to-back launches, the
+        // stores themselves ~1 us slower, overlapped with other workgroups)
 #pragma unroll
         for (int it = 0; it < WTM / RPI; ++it) {
             const int m = it * RPI + lane / CPRW, c = lane % CPRW;
             const u32x4 v = *reinterpret_cast<const lds_u32x4*>((size_t)(wbase + m * PITCH + c * 16));
             const int gm = wrow0 + m, gn = wcol0 + 8 * c;
-            if (gm < M && gn < N) *reinterpret_cast<u32x4*>(C + (int64_t)gm * N + gn) = v;
+            if (gm < M && gn < N) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + (int64_t)gm * N + gn));
         }
+        ts_end();
         return;
     }
     // ---- epilogue with beta: read-modify-write straight from the accumulators.
@@ -452,6 +507,20 @@ __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
             }
         }
     }
+    ts_end();
+}
+
+// (a template so that every translation unit that includes this header can
+// see it without defining the kernel twice; launched as gemm_f16_big<Big>)
+template <class CF>
+__global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
+    big_body<CF, false>(p, nullptr);
+}
+
+// the same kernel with the phase timestamps (ts: kTsWords words per workgroup)
+template <class CF>
+__global__ void __launch_bounds__(CF::NT) gemm_f16_big_ts(Args p, unsigned long long* ts) {
+    big_body<CF, true>(p, ts);
 }
 
 }  // namespace dma

@@ -276,7 +276,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_i8_big(Args p) {
         const int m = it * RPI + lane / CPRW, c = lane % CPRW;
         const u32x4 v = *reinterpret_cast<const lds_u32x4*>((size_t)(wbase + m * PITCH + c * 16));
         const int gm = wrow0 + m, gn = wcol0 + 8 * c;
-        if (gm < M && gn < N) *reinterpret_cast<u32x4*>(C + (int64_t)gm * N + gn) = v;
+        // nontemporal, as in the FP16 kernel: no dirty C in L2 at the kernel's end
+        if (gm < M && gn < N) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(C + (int64_t)gm * N + gn));
     }
 }
 
