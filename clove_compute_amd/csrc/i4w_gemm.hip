@@ -19,6 +19,16 @@ using CfgBig = Cfg<4, 1, 2, 4, 3>;  // 256 x 128, 4 waves of 64 x 128
 // 125.6 -> 122.9 us, fused 114.9 -> 111.1 us against three stages)
 using CfgC64 = Cfg<4, 1, 1, 2, 2>;
 using CfgC32 = Cfg<2, 1, 1, 1, 4>;  // 64 x 32, 2 waves (several workgroups per CU)
+// 256 x 64 (four waves of 64 x 64), one stage ahead (70 KB LDS: two workgroups
+// per CU): the fused gate/up + SwiGLU from 512 X rows up, where each wave's two
+// weight blocks (a gate and an up block per 32 outputs) share every X
+// fragment it reads.  Measured against 128 x 64 / 256 x 128 on the Llama-1B
+// and -7B MLPs (I x K = 8192 x 2048, 11008 x 4096; graph replays, cold
+// weights), T = 512 (alternating blocks): 47.0-48.0 -> 45.0-45.2 and
+// 119.3-119.8 -> 116.6-117.2 us, T = 1024: 94.8 -> 85.9 and 224.6 -> 217.2,
+// T = 2048: 184.2 -> 166.2 and 470.8 -> 420.1; at T <= 256 it loses (T = 64:
+// 14.6 -> 19.3)
+using CfgS64 = Cfg<4, 1, 2, 2, 2>;
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -81,12 +91,13 @@ clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_byt
 //   otherwise 128 x 64 with two workgroups per CU, whose waves interleave
 //   VALU (unpack, fold) with MFMA -- ahead of 128 x 128 by 15-25 % on the
 //   INT4 N = 128 and W4A16 T = 512 shapes -- unless 256 x 128 tiles already
-//   cover the CUs (large prefill)
+//   cover the CUs (large prefill); the fused SwiGLU from 512 X rows up: 256 x 64
 // Splits keep at least 10 (64 x 32) or 8 groups each.
 template <bool XS, int OUT, class Prep>
 clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t stream, Prep prep) {
     const int rows = OUT == 2 ? 2 * a.R : a.R;  // weight rows
     if (a.C <= 32) return run<CfgC32, XS, OUT>(a, cus, 3 * cus, 10, extra_bytes, stream, prep);
+    if (OUT == 2 && a.C >= 512) return run<CfgS64, XS, OUT>(a, cus, 2 * cus, 8, extra_bytes, stream, prep);
     // (SwiGLU tiles pair gate and up rows: the same outputs take twice the
     // weight rows, so the big tile waits for twice the grid)
     if (cdiv(rows, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= (OUT == 2 ? 2 : 1) * cus)

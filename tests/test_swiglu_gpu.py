@@ -131,7 +131,8 @@ def check_rows(X, Wq, s, z, H, rows):
 # MLP (I = 8192, K = 2048) at decode and prefill
 @pytest.mark.parametrize("T,I,K", [(1, 8192, 2048), (2, 300, 1024), (3, 64, 256), (4, 1000, 4096),
                                    (5, 8192, 2048), (17, 200, 512), (33, 1000, 1024), (64, 96, 2048),
-                                   (100, 777, 384), (512, 8192, 2048), (1, 2000, 4096), (1, 1100, 8192)])
+                                   (100, 777, 384), (512, 8192, 2048), (1, 2000, 4096), (1, 1100, 8192),
+                                   (600, 520, 1024), (1030, 136, 256)])
 def test_w4a16_swiglu_shapes(T, I, K):
     X, Wq, s, z, g = make_gate_up(T, I, K, "shapes")
     H = run_w4a16_swiglu(X, Wq, s, z, I)
@@ -148,7 +149,8 @@ def test_w4a16_swiglu_composed_fallback(T, I, K, x_offset):
     check_rows(X, Wq, s, z, H, np.arange(T))
 
 
-@pytest.mark.parametrize("T,I,K", [(1, 512, 1024), (4, 96, 256), (48, 256, 512), (300, 640, 768)])
+@pytest.mark.parametrize("T,I,K", [(1, 512, 1024), (4, 96, 256), (48, 256, 512), (300, 640, 768),
+                                   (512, 640, 768)])
 def test_w4a16_swiglu_exact_inputs(T, I, K):
     # gate and up are exact: the only freedom left is expf's last fp32 bit
     X, Wq, s, z, _ = make_gate_up(T, I, K, "pow2", pow2=True)
