@@ -26,6 +26,7 @@ using F16T64 = Cfg<false, 64, 64, 2, 2, 6>;
 using F16T64S2 = Cfg<false, 64, 64, 2, 2, 2>;
 using I8M32 = Cfg<true, 32, 128, 1, 4, 5>;
 using I8M128 = Cfg<true, 128, 64, 4, 1, 4>;
+using I8T128 = Cfg<true, 128, 128, 2, 2, 3>;
 
 template <class CF, int OUT>
 clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
@@ -83,6 +84,12 @@ F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
         return (t128 >= cus / 2 || long_k) ? F16Tile::kT128 : F16Tile::kT64;
     }
     if (M > 128 && long_k && N >= 4096) return F16Tile::kT128;
+    // and for 64 < M <= 128 on wide weights (N >= 10240, K >= 4096), in two K
+    // splits: half the A-panel bytes per workgroup of the 128x64 tiles (cold,
+    // 128 x 11008 x 4096 35.1 -> 30.2 us, 96 x 11008 x 4096 31.2 -> 28.5,
+    // 80 x 11008 x 4096 30.8 -> 27.7, 128 x 14336 x 4096 39.0 -> 34.1; not at
+    // N = 8192, K = 2048 or N = 4096, K = 11008, where 128x64 stays ahead)
+    if (M > 64 && M <= 128 && long_k && N >= 10240) return F16Tile::kT128;
     // 32-row tiles up to M = 64 (cold 4096 x 4096 weights: M = 40 / 48 / 64 at
     // 13.6 / 14.1 / 14.5 us against 14.9 / 15.3 / 15.5 with 64-row tiles), and
     // for short K with few 128-row tiles, where they make 4x the workgroups
@@ -193,6 +200,9 @@ bool try_skinny_int8(const Int8Args& q, int cus, hipStream_t stream, clove_statu
                              (int64_t)cdiv(q.M, I8M128::BM) * cdiv(q.N, I8M128::BN) < cus / 2;
         const bool large_w = (int64_t)q.N * q.K > ((int64_t)32 << 20);
         if (q.M <= 64 || (q.M <= 128 && !large_w) || short_k) return run<I8M32, OUT>(a, 1, cus, stream);
+        // 128x128 tiles for M <= 128 on wide weights, as for FP16 (cold, 128 x
+        // 11008 x 4096 23.7 -> 20.5 us; 128 x 4096 x 11008 stays on 128x64)
+        if (q.M <= 128 && q.N >= 10240 && q.K >= 4096) return run<I8T128, OUT>(a, 1, cus, stream);
         return run<I8M128, OUT>(a, 1, cus, stream);
     };
     switch (q.out) {

@@ -289,7 +289,7 @@ def test_mid_size_tiles(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (1024, 1024, 1024), (600, 392, 320), (192, 11008, 4096),
-                                   (384, 4096, 4096), (160, 1000, 2048)])
+                                   (384, 4096, 4096), (160, 1000, 2048), (128, 11008, 4096), (96, 10240, 4096)])
 def test_mid_size_tiles_small_integers_bit_exact(M, N, K):
     g = rng("mid-int", M, N, K)
     A = g.integers(-2, 3, (M, K)).astype(np.float16)

@@ -60,6 +60,7 @@ def test_config3_w8a8_rowcol(M):
     (1, 4096, 4096, 0, 0), (1, 512, 1000, 3, -5), (3, 256, 256, -128, 127), (4, 96, 64, 7, 7),
     (64, 64, 64, 0, 0), (200, 130, 300, 5, -9), (129, 4096, 512, -3, 2), (37, 19, 45, 1, 1),
     (512, 512, 512, 0, 0), (1000, 1024, 1024, 0, 0), (2048, 256, 2048, 0, 0), (96, 11008, 4096, 0, 0),
+    (128, 11008, 4096, 0, 0), (100, 10240, 4096, 0, 0),
 ])
 def test_per_tensor_bit_exact(M, N, K, za, zb):
     g = rng("pt", M, N, K, za, zb)

@@ -233,7 +233,7 @@ def test_swiglu_fused_fp16(T, H, I):
 @pytest.mark.parametrize("T,H,I", [(1, 2048, 8192), (2, 1024, 512), (4, 4096, 264), (7, 64, 96),
                                    (40, 1024, 520), (64, 512, 1000), (128, 4096, 1024), (300, 512, 768),
                                    (512, 2048, 8192), (3, 4096, 4096), (2, 4096, 11008),
-                                   (1024, 2048, 8192), (2048, 4096, 11008)])
+                                   (1024, 2048, 8192), (2048, 4096, 11008), (96, 4096, 10240)])
 def test_swiglu_fused_equals_gemms_then_swiglu(T, H, I):
     # the fused kernels sum gate and up in the order gemm_fp16 does for the
     # same shape (same kernel family, tiles and split plan: the GEMV, or the
