@@ -23,7 +23,7 @@ CLOVE_ERR_WORKSPACE = 8
 CLOVE_ERR_SCRATCH_LIMIT = 9
 
 CLOVE_WORKSPACE_MIN_BYTES = 65536
-CLOVE_NOALLOC_SCRATCH_BYTES = 32 << 20
+CLOVE_NOALLOC_SCRATCH_BYTES = 65 << 20
 
 CLOVE_INT4_GROUPWISE = 0
 CLOVE_INT4_REFERENCE_LITERAL = 1

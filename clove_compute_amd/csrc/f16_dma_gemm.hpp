@@ -64,6 +64,14 @@ struct Args {
     float alpha, beta;
     int64_t sA, sB, sC;  // batch strides (elements)
     int tiles_m, tiles_n;
+    // the K split (gemm_f16_big_split, one batch): workgroup r takes K tiles
+    // [s ktps, (s + 1) ktps) of tile r / nsplit, s = r % nsplit, publishes its
+    // fp32 partial tile to `part` (slab r) and counts in `counters` (one per
+    // tile); the last to arrive sums the partials in split order and stores
+    // the tile
+    int nsplit, ktps;
+    float* part;
+    unsigned* counters;
 };
 
 // s_waitcnt with only the vector-memory counter constrained
@@ -214,6 +222,17 @@ constexpr bool plan_valid() {
 }
 static_assert(plan_valid(), "slot plan");
 
+// tile `tile` of one batch: the tiles are walked 8 tile-rows at a time
+__device__ __forceinline__ void tile_rc(const Args& p, int tile, int& tm, int& tn) {
+    constexpr int GM = 8;
+    const int group = tile / (GM * p.tiles_n);
+    const int first_m = group * GM;
+    const int gm = min(p.tiles_m - first_m, GM);
+    const int in_group = tile - group * GM * p.tiles_n;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
 __device__ __forceinline__ void tile_coords(const Args& p, int& batch, int& tm, int& tn) {
     int bid = blockIdx.x;
     const int nblk = gridDim.x;
@@ -222,14 +241,7 @@ __device__ __forceinline__ void tile_coords(const Args& p, int& batch, int& tm, 
     if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
     const int per_batch = p.tiles_m * p.tiles_n;
     batch = bid / per_batch;
-    int tile = bid - batch * per_batch;
-    constexpr int GM = 8;
-    const int group = tile / (GM * p.tiles_n);
-    const int first_m = group * GM;
-    const int gm = min(p.tiles_m - first_m, GM);
-    const int in_group = tile - group * GM * p.tiles_n;
-    tm = first_m + in_group % gm;
-    tn = in_group / gm;
+    tile_rc(p, bid - batch * per_batch, tm, tn);
 }
 
 typedef short i16x4v __attribute__((vector_size(8)));
@@ -268,7 +280,7 @@ enum TsSlot : int { kTsEntry = 0, kTsFirst = 2, kTsTwo = 4, kTsLoop = 6, kTsEnd 
 // s_memtime / s_memrealtime reads at the phase boundaries (whose results the
 // compiler waits for with the LDS reads in flight at that point) and one
 // store per workgroup after the output stores.
-template <class CF, bool TS>
+template <class CF, bool TS, bool SPLIT = false>
 __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) {
     using Big = CF;
     unsigned long long tsv[10] = {};
@@ -281,14 +293,26 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
     constexpr int A_BYTES = Big::A_BYTES, B_BYTES = Big::B_BYTES;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[Big::LDS_BYTES / 2];
 
+    const int M = p.M, N = p.N, K = p.K;
+    const int KT = K / BK;
     int batch, tm, tn;
-    tile_coords(p, batch, tm, tn);
+    // this workgroup's K tiles [kbeg, kend); SPLIT: part `split` of tile rtile
+    int kbeg = 0, kend = KT, rtile = -1, split = 0;
+    if constexpr (SPLIT) {
+        const int r = blockIdx.x;
+        batch = 0;
+        rtile = r / p.nsplit;
+        split = r - rtile * p.nsplit;
+        tile_rc(p, rtile, tm, tn);
+        kbeg = split * p.ktps;
+        kend = min(KT, kbeg + p.ktps);
+    } else {
+        tile_coords(p, batch, tm, tn);
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = tm * BM, n0 = tn * BN;
-    const int M = p.M, N = p.N, K = p.K;
-    const int KT = K / BK;
 
     const u32x4 ra = make_rsrc(p.A + batch * p.sA, (unsigned)M * K * 2);
     const u32x4 rb = make_rsrc(p.B + batch * p.sB, (unsigned)K * N * 2);
@@ -339,13 +363,14 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
     f16x8 fa[2][FM];
     u32x2 fb[FN][2];
 
-    // ---- prologue: A(0), B(0), A(1), B(1) in flight in that order (the waits
-    // below count on it), the first two landed, k-step 0 fragments of tile 0 ----
+    // ---- prologue: A(kbeg), B(kbeg), A(kbeg + 1), B(kbeg + 1) in flight in that
+    // order (the waits below count on it), the first two landed, k-step 0
+    // fragments of tile kbeg ----
 #pragma unroll
-    for (int i = 0; i < Big::DMA_A; ++i) dma_a(0, 0, i);
+    for (int i = 0; i < Big::DMA_A; ++i) dma_a(kbeg, 0, i);
 #pragma unroll
-    for (int i = 0; i < Big::DMA_B; ++i) dma_b(0, 0, i);
-    const int k1 = min(1, KT - 1);
+    for (int i = 0; i < Big::DMA_B; ++i) dma_b(kbeg, 0, i);
+    const int k1 = min(kbeg + 1, kend - 1);
 #pragma unroll
     for (int i = 0; i < Big::DMA_A; ++i) dma_a(k1, 1, i);
 #pragma unroll
@@ -369,7 +394,7 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
         constexpr int P = decltype(PC)::value;
         const int ast1 = ast == 2 ? 0 : ast + 1;
         const int ast2 = ast1 == 2 ? 0 : ast1 + 1;
-        const int k2 = min(kt + 2, KT - 1);
+        const int k2 = min(kt + 2, kend - 1);
         // opaque per tile, so the B read addresses fold into instruction offsets
         unsigned bcur = lds_b + P * B_BYTES, bnext = lds_b + (P ^ 1) * B_BYTES;
         asm volatile("" : "+v"(bcur), "+v"(bnext));
@@ -401,9 +426,9 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
             }
         ast = ast1;
     };
-    int kt = 0;
+    int kt = kbeg;
 #pragma unroll 1
-    for (; kt + 1 < KT; kt += 2) {
+    for (; kt + 1 < kend; kt += 2) {
         if constexpr (TS) {
             if (kt == 2) {
                 tsv[kTsTwo] = __builtin_amdgcn_s_memtime();
@@ -413,10 +438,80 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
         tile(kt, IntC<0>{});
         tile(kt + 1, IntC<1>{});
     }
-    if (kt < KT) tile(kt, IntC<0>{});  // odd K / 64
+    if (kt < kend) tile(kt, IntC<0>{});  // odd number of K tiles
     // every DMA has landed and every wave is done with the stages
     stage_barrier<vmcnt_imm(0)>();
     acc_fence<1>(acc);  // the last MFMA results land before the accumulators are read
+    if constexpr (SPLIT) {
+        {
+            // publish this split's partial tile; the last split to arrive sums
+            // them in split order and runs the epilogue
+            constexpr int NC = FN * FM;
+            float* slabs = p.part + (size_t)rtile * p.nsplit * (NC * Big::NT * 4);
+            splitk_publish<NC, Big::NT>(slabs + (size_t)split * (NC * Big::NT * 4), tid, acc);
+            // (the stages are dead: every DMA was waited for, every read returned)
+            if (!splitk_arrive_is_last(p.counters + rtile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
+                return;
+            // the sum in split order (((p0 + p1) + p2) + ..., every part read
+            // back, this split's own too, so that the accumulators are dead
+            // here), then the alpha / beta epilogue straight from the sums:
+            // lane holds m = 16 j + q, n = 16 i + 4 h + 0..3 of tile (i, j) =
+            // chunk 8 i + j.  Two parts: 16 chunks of both per round trip;
+            // more: 8 chunks of one part per round trip.
+            constexpr int CG = 16;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                slabs, (short)0, p.nsplit * NC * Big::NT * 16, 0x00020000);
+            const int wr0 = m0 + wm * WTM, wc0 = n0 + wn * WTN;
+            const int qq = lane & 15, hh = lane >> 4;
+            auto ld = [&](int sp, int c) {
+                return bitcast<f32x4>(
+                    __builtin_amdgcn_raw_buffer_load_b128(rs, ((sp * NC + c) * Big::NT + tid) * 16, 0, kCpolSc1));
+            };
+#pragma unroll
+            for (int c0 = 0; c0 < NC; c0 += CG) {
+                f32x4 sum[CG];
+                if (p.nsplit == 2) {
+                    f32x4 t1[CG];
+#pragma unroll
+                    for (int c = 0; c < CG; ++c) {
+                        sum[c] = ld(0, c0 + c);
+                        t1[c] = ld(1, c0 + c);
+                    }
+#pragma unroll
+                    for (int c = 0; c < CG; ++c) sum[c] += t1[c];
+                } else {
+#pragma unroll
+                    for (int h8 = 0; h8 < CG; h8 += 8) {
+                        for (int sp = 0; sp < p.nsplit; ++sp) {
+                            f32x4 t[8];
+#pragma unroll
+                            for (int c = 0; c < 8; ++c) t[c] = ld(sp, c0 + h8 + c);
+#pragma unroll
+                            for (int c = 0; c < 8; ++c) sum[h8 + c] = sp == 0 ? t[c] : sum[h8 + c] + t[c];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CG; ++c) {
+                    const int i = (c0 + c) >> 3, j = (c0 + c) & 7;
+                    const int gm = wr0 + 16 * j + qq, gn = wc0 + 16 * i + 4 * hh;
+                    if (gm >= M || gn >= N) continue;
+                    uint16_t* dst = p.C + (int64_t)gm * N + gn;
+                    const f32x4 v = sum[c];
+                    float r[4] = {p.alpha * v[0], p.alpha * v[1], p.alpha * v[2], p.alpha * v[3]};
+                    if (p.beta != 0.0f) {
+                        const u32x2 old = *reinterpret_cast<const u32x2*>(dst);
+                        r[0] = fmaf(p.beta, h2f(old.x & 0xffffu), r[0]);
+                        r[1] = fmaf(p.beta, h2f(old.x >> 16), r[1]);
+                        r[2] = fmaf(p.beta, h2f(old.y & 0xffffu), r[2]);
+                        r[3] = fmaf(p.beta, h2f(old.y >> 16), r[3]);
+                    }
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(r[0], r[1]), pack2h(r[2], r[3])};
+                }
+            }
+            return;
+        }
+    }
     if constexpr (TS) {
         tsv[kTsLoop] = __builtin_amdgcn_s_memtime();
         tsv[kTsLoop + 1] = __builtin_amdgcn_s_memrealtime();
@@ -515,6 +610,12 @@ __device__ __forceinline__ void big_body(const Args& p, unsigned long long* ts) 
 template <class CF>
 __global__ void __launch_bounds__(CF::NT) gemm_f16_big(Args p) {
     big_body<CF, false>(p, nullptr);
+}
+
+// the K split (Args: nsplit, ktps, part, counters)
+template <class CF>
+__global__ void __launch_bounds__(CF::NT) gemm_f16_big_split(Args p) {
+    big_body<CF, false, true>(p, nullptr);
 }
 
 // the same kernel with the phase timestamps (ts: kTsWords words per workgroup)

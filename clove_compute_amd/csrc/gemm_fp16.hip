@@ -254,12 +254,48 @@ bool dma_eligible(const void* A, const void* B, const void* C, int M, int N, int
            (int64_t)K * N * 2 < (1ll << 31) && (int64_t)M * N * 2 < (1ll << 31);
 }
 
+// The K split of the 256x256 kernel.  When its tiles cover only half the CUs
+// (the kernel is chosen from cus / 2 tiles up; M x N = 128 tiles of 256 x 256
+// on this part, e.g. 2048 x 4096) and K is long, each tile's K range is split
+// in two: every CU runs a half-length tile, both halves publish fp32 partial
+// tiles (256 KB each) and the last to arrive sums them in split order.
+// Measured against the same 128 tiles unsplit: K = 11008 164-169 against
+// 207-210 us; K = 4096 82-84 against 84-102 (half the chip idle runs at a
+// higher clock), so only from K = 8192.  Not above cus / 2 tiles: splitting
+// the remainder of a partly filled last round (2048 x 11008 x 4096, 344 tiles)
+// measured no faster (185.6 against 187.8 us), the partials' traffic (1 MB per
+// split tile) costing what the shorter round saved.
+struct BigSplit {
+    int nsplit = 1, ktps = 0;
+};
+BigSplit big_split_plan(int64_t tiles, int batch, int KT, int cus) {
+    BigSplit sp;
+    if (batch != 1 || 2 * tiles > cus || KT < 128) return sp;
+    sp.ktps = cdiv(KT, 2);
+    sp.nsplit = cdiv(KT, sp.ktps);
+    return sp;
+}
+
 clove_status_t run_dma(const uint16_t* A, const uint16_t* B, uint16_t* C, int batch, int M, int N,
-                       int K, float alpha, float beta, hipStream_t stream) {
+                       int K, float alpha, float beta, int cus, hipStream_t stream) {
     dma::Args a{A, B, C, M, N, K, alpha, beta, (int64_t)M * K, (int64_t)K * N, (int64_t)M * N,
                 cdiv(M, BigTile::BM), cdiv(N, BigTile::BN)};
     const int64_t grid = (int64_t)a.tiles_m * a.tiles_n * batch;
     if (grid > 0x7fffffff) return CLOVE_ERR_INVALID_DIM;
+    const BigSplit sp = big_split_plan(grid, batch, K / BigTile::BK, cus);
+    if (sp.nsplit > 1) {
+        constexpr size_t kSlab = (size_t)BigTile::FM * BigTile::FN * BigTile::NT * 16;  // one part's tile
+        Scratch s;
+        const clove_status_t st = acquire_scratch(stream, (size_t)grid * sp.nsplit * kSlab, (size_t)grid, &s);
+        if (st != CLOVE_OK) return st;
+        a.nsplit = sp.nsplit;
+        a.ktps = sp.ktps;
+        a.part = s.partials;
+        a.counters = s.counters;
+        CLOVE_LAUNCH(dma::gemm_f16_big_split<dma::Big>, dim3((unsigned)(grid * sp.nsplit)), dim3(BigTile::NT), 0,
+                     stream, a);
+        return check_launch();
+    }
     CLOVE_LAUNCH(dma::gemm_f16_big<dma::Big>, dim3((unsigned)grid), dim3(BigTile::NT), 0, stream, a);
     return check_launch();
 }
@@ -335,7 +371,7 @@ clove_status_t launch_gemm_fp16(const uint16_t* A, const uint16_t* B, uint16_t* 
     const int cus = dev.num_cus;
     const int64_t big_tiles = (int64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
     if (big_tiles >= cus / 2 && dma_eligible(A, B, C, M, N, K))
-        return run_dma(A, B, C, batch, M, N, K, alpha, beta, stream);
+        return run_dma(A, B, C, batch, M, N, K, alpha, beta, cus, stream);
     {
         clove_status_t st2;
         if (try_skinny_fp16(A, B, C, batch, M, N, K, alpha, beta, cus, stream, &st2)) return st2;

@@ -280,8 +280,8 @@ size_t clove_workspace_query_end(void);
  * library's static device memory, held until the process ends); a call that
  * would need more returns CLOVE_ERR_SCRATCH_LIMIT and launches nothing.
  * Every shape with M <= 512 and N, K <= 8192 whose operands are 16-byte
- * aligned, with N % 8 == 0 and K % 64 == 0, fits, as do the large shapes
- * (M, N >= 2048) that split nothing.  The first call on a device clears the array's counters
+ * aligned, with N % 8 == 0 and K % 64 == 0, fits, as does every shape on the
+ * 256x256 tile (its K split needs at most 64 MiB of partials).  The first call on a device clears the array's counters
  * with one small kernel on `stream`.  Every call on a GPU shares that GPU's
  * array: calls that may overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.  Inside a workspace
@@ -289,7 +289,7 @@ size_t clove_workspace_query_end(void);
  * CLOVE_ERR_SCRATCH_LIMIT for a call the array cannot hold, and leaves the
  * query's size as it was (the array is not the caller's workspace).
  */
-#define CLOVE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+#define CLOVE_NOALLOC_SCRATCH_BYTES ((size_t)65 << 20)
 clove_status_t clove_gemm_fp16_noalloc(const void* A, const void* B, void* C,
                                        int M, int N, int K, float alpha, float beta,
                                        void* stream);

@@ -218,6 +218,34 @@ def test_big_tile_batched():
         assert ok, (b, rep)
 
 
+# the 256x256 kernel's K split: where its tiles cover only half the CUs (128
+# tiles) and K >= 8192, each tile's K range in two parts, fp32 partials summed
+# in split order by the last part (even and odd K-tile counts, ragged M and
+# N); 128 tiles with shorter K and partly filled last rounds (344 and 288
+# tiles) are not split
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 8192), (1900, 4000, 8256), (2048, 4096, 1024), (2048, 11008, 1024),
+                                   (1800, 9000, 1024)])
+def test_big_tile_k_split_small_integers_bit_exact(M, N, K):
+    g = rng("big_split_int", M, N, K)
+    A = g.integers(-3, 4, (M, K)).astype(np.float16)
+    B = g.integers(-3, 4, (K, N)).astype(np.float16)
+    C = run_fp16(A, B)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.array_equal(f16bits(C), f16bits(exact.astype(np.float16)))
+
+
+@pytest.mark.parametrize("M,N,K,alpha,beta", [(2048, 4096, 11008, 1.0, 0.0), (1900, 4000, 8256, 0.5, 0.75)])
+def test_big_tile_k_split(M, N, K, alpha, beta):
+    g = rng("big_split", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.02).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16) if beta != 0.0 else None
+    C = run_fp16(A, B, C0, alpha, beta)
+    rows = np.unique(np.concatenate([[0, 255, 256, M - 256, M - 1], g.integers(0, M, 24)]))
+    check_rows(A, B, C, rows, C0, alpha, beta)
+    assert np.all(np.isfinite(C.astype(np.float32)))
+
+
 def test_big_shape_k_not_multiple_of_tile():
     # K % 64 != 0 takes the generic MFMA kernel
     M, N, K = 4096, 4096, 1000

@@ -51,9 +51,10 @@ def test_noalloc_equals_gemm_fp16_two_calls():
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (32, 4096, 4096), (512, 4096, 4096), (300, 1000, 640),
-                                   (77, 45, 131), (4096, 4096, 4096)])
+                                   (77, 45, 131), (4096, 4096, 4096), (2048, 4096, 8192), (1900, 4000, 8256)])
 def test_noalloc_shapes(M, N, K):
-    # the GEMV, skinny, mid-size, generic (unaligned) and 256x256 kernels
+    # the GEMV, skinny, mid-size, generic (unaligned) and 256x256 kernels, and
+    # the 256x256 kernel's K split (its 64 MiB of partials in the fixed array)
     ref, got = _run_pair(M, N, K, "shapes", 0.25)
     assert np.array_equal(f16bits(got), f16bits(ref))
 
@@ -71,7 +72,7 @@ def _query_need(M, N, K, A, B, C):
 def test_noalloc_rejects_calls_beyond_its_array():
     import torch
     import clove_compute_amd as cg
-    M, N, K = 4, 32768, 32768  # GEMV partials: 128 column blocks x 128 splits x 4 rows x 1 KB
+    M, N, K = 4, 36864, 32768  # GEMV partials: 144 column blocks x 128 splits x 4 rows x 1 KB (72 MiB)
     A = empty_f16(M, K)
     B = torch.zeros(K, N, dtype=torch.float16, device="cuda")
     C = empty_f16(M, N, fill=float("nan"))
@@ -109,11 +110,11 @@ def test_noalloc_in_a_size_query():
     from clove_compute_amd import _lib
     L = _lib.lib()
     A = empty_f16(4, 32768)
-    B = torch.zeros(32768, 32768, dtype=torch.float16, device="cuda")
-    C = empty_f16(4, 32768, fill=float("nan"))
+    B = torch.zeros(32768, 36864, dtype=torch.float16, device="cuda")
+    C = empty_f16(4, 36864, fill=float("nan"))
     A2, B2, C2 = empty_f16(128, 4096), empty_f16(4096, 4096), empty_f16(128, 4096)
     assert L.clove_workspace_query_begin() == 0
-    big = _abi("clove_gemm_fp16_noalloc", A, B, C, 4, 32768, 32768)
+    big = _abi("clove_gemm_fp16_noalloc", A, B, C, 4, 36864, 32768)
     fits = _abi("clove_gemm_fp16_noalloc", A2, B2, C2, 128, 4096, 4096)
     need = L.clove_workspace_query_end()
     assert big == cg.CLOVE_ERR_SCRATCH_LIMIT
