@@ -123,14 +123,20 @@ __device__ __forceinline__ void dma4(const u32x4& rsrc, unsigned lds_addr, int v
                  : "memory");
 }
 
-// (q - z) * 2^-9 for the 8 nibbles of one dword, in k order; zz = -z * 2^-9
+// (q - z) * 2^-9 for the 8 nibbles of one dword, in k order; zz = -z * 2^-9.
+// Byte b holds k = 2b and 2b + 1: in the high and low nibble (the weights'
+// packing), or with LO_FIRST in the low and high nibble (the order in which
+// ds_read_b64_tr_b4 returns k rows)
+template <bool LO_FIRST = false>
 __device__ __forceinline__ f16x8 unpack8(unsigned w, f16x2 zz) {
     const unsigned hr = w & 0xf0f0f0f0u, lo = w & 0x0f0f0f0fu;
-    const f16x2 mul = {(_Float16)2048.0f, (_Float16)32768.0f};
+    const f16x2 mul = LO_FIRST ? f16x2{(_Float16)32768.0f, (_Float16)2048.0f}
+                               : f16x2{(_Float16)2048.0f, (_Float16)32768.0f};
     f16x2 v[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        const unsigned sel = 0x0c000c00u | (unsigned)b | ((unsigned)(4 + b) << 16);
+        const unsigned sel = LO_FIRST ? 0x0c000c00u | (unsigned)(4 + b) | ((unsigned)b << 16)
+                                      : 0x0c000c00u | (unsigned)b | ((unsigned)(4 + b) << 16);
         const f16x2 sub = bitcast<f16x2>(__builtin_amdgcn_perm(lo, hr, sel));
         v[b] = __builtin_elementwise_fma(sub, mul, zz);
     }

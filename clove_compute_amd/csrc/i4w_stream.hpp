@@ -27,13 +27,17 @@
 //
 // RAWB (group-wise INT4 with 15 or 16 columns): no transpose pre-pass.  B
 // [K, 8] bytes (16 nibbles per k row) is contiguous, so each wave copies the
-// 1 KB of every group it owns into LDS by LDS DMA at the start and reorders
-// it there once, in place: an 8 x 8 nibble transpose (three stages of masked
-// swaps of 16-, 8- and 4-bit fields) turns the 8 rows k = 32 q + 8 h .. + 7 of
-// 8 columns into one dword per column in the weights' nibble order, stored
-// so that lane (h, column) finds the dwords of its four steps in one 16-byte
-// slot.  They are unpacked with the same exact (q - z) 2^-9 arithmetic; the
-// extra 2^-9 is returned in the fold.
+// 1 KB of every group it owns into LDS in k-row order at the start, and
+// gfx950's ds_read_b64_tr_b4 transposes it on the way out: within a 16-lane
+// group, result lane j gets nibble j of the 16 source lanes' 8-byte rows,
+// i.e. 16 consecutive k of one column (nibble j of a row is column j ^ 1: the
+// even column sits in the high nibble), so lane l's X row is column
+// (l % 16) ^ 1.  Two such reads give lane group h the k = 32 h .. 32 h + 31 of
+// the group, and step q uses k = 32 h + 8 q .. + 7 -- the order in which the
+// weights' 16-byte group slices arrive, so with raw B the weights need no
+// lane-group transpose either.  B nibbles come out with the even k in the
+// low nibble (unpack8<true>), and are unpacked with the same exact
+// (q - z) 2^-9 arithmetic; the extra 2^-9 is returned in the fold.
 #pragma once
 
 #include "i4w_gemm.hpp"
@@ -67,34 +71,19 @@ __device__ __forceinline__ u32x4 transpose_lane_groups(u32x4 v) {
     return u32x4{c[0], d[0], c[1], d[1]};
 }
 
-// 8 x 8 transpose of 4-bit fields: nibble j of x[i] goes to nibble i of x[j]
-// (three stages of field swaps between registers 4, 2 and 1 apart)
-__device__ __forceinline__ void nibble_transpose8(unsigned (&x)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const unsigned a = x[i], b = x[i + 4];
-        x[i] = (a & 0x0000ffffu) | (b << 16);
-        x[i + 4] = (a >> 16) | (b & 0xffff0000u);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = (j & 1) + 4 * (j >> 1);  // 0, 1, 4, 5
-        const unsigned a = x[i], b = x[i + 2];
-        x[i] = (a & 0x00ff00ffu) | ((b << 8) & 0xff00ff00u);
-        x[i + 2] = ((a >> 8) & 0x00ff00ffu) | (b & 0xff00ff00u);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-        const unsigned a = x[i], b = x[i + 1];
-        x[i] = (a & 0x0f0f0f0fu) | ((b << 4) & 0xf0f0f0f0u);
-        x[i + 1] = ((a >> 4) & 0x0f0f0f0fu) | (b & 0xf0f0f0f0u);
-    }
+typedef int i32x2v __attribute__((vector_size(8)));
+typedef __attribute__((address_space(3))) i32x2v lds_i32x2v;
+
+// ds_read_b64_tr_b4 at LDS byte address a (see the RAWB note above)
+__device__ __forceinline__ u32x2 lds_read_tr4(unsigned a) {
+    const i32x2v v = __builtin_amdgcn_ds_read_tr4_b64_v2i32(reinterpret_cast<lds_i32x2v*>((size_t)a));
+    return u32x2{(unsigned)v[0], (unsigned)v[1]};
 }
 
 template <class SC, bool XS, int OUT, bool RAWB = false>
 __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     constexpr int WF = SC::WF, XF = SC::XF, NG = SC::NG, D = SC::D, ROWS = SC::ROWS;
-    static_assert(!RAWB || (XS && XF == 1), "raw B: group-wise INT4, 16 columns");
+    static_assert(!RAWB || (XS && XF == 1 && OUT == 0), "raw B: group-wise INT4, 16 columns");
     extern __shared__ __attribute__((aligned(16))) float red[];
 
     const int tid = threadIdx.x, lane = tid & 63, h = lane >> 4, l16 = lane & 15;
@@ -123,7 +112,7 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
     // DMA: loads complete in order, so the wait for these waits for nothing
     // issued after them, where a read of LDS behind an LDS DMA waits for every
     // outstanding load, the weight stream included.  (A wave without groups
-    // loads group G - 1 and stores none of it.)
+    // loads group G - 1, see the staging below.)
     u32x4 braw[RAWB ? NG : 1];
     if constexpr (RAWB) {
 #pragma unroll
@@ -153,107 +142,88 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
         }
     };
 
-    // ---- the workgroup's scales, zero points and sx to LDS; their loads go
-    // out first, so that waiting for them does not wait for the weight stream
-    // issued right behind ----
-    constexpr int SPT = 8;  // staged elements per thread per pass
-    const int nsz = ROWS * G;
-    const int nxs = XS ? G * 16 * XF : 0;
-    uint16_t sv[SPT], zv[SPT], sbv[SPT] = {}, zbv[SPT] = {};
-    float xv[SPT] = {};
-    // unconditional loads from clamped addresses (a guarded load becomes a
-    // branch whose merge waits for it, and for everything issued before it)
-    auto stage_load = [&](int base) {
+    // ---- this wave's scales and zero points (and sx, or sB / zB) to LDS.
+    // Every wave stages exactly the constants of the groups it computes (a
+    // wave without groups those of group G - 1, the same values its owner
+    // writes), so no wave waits for another before its K loop: one wave's LDS
+    // accesses take effect in program order.  The loads go out first, so that
+    // waiting for them does not wait for the weight stream issued right
+    // behind; they are unconditional, from clamped addresses (a guarded load
+    // becomes a branch whose merge waits for it, and for everything issued
+    // before it) ----
+    const int gs0 = g0 < G ? g0 : G - 1;      // first staged group
+    const int ngs = g0 < G ? g1 - g0 : 1;     // staged groups, 1..NG
+    constexpr int SPL = (ROWS * NG + 63) / 64;                 // weight constants per lane
+    constexpr int XPL = XS ? (16 * XF * NG + 63) / 64 : 1;     // sx entries per lane
+    uint16_t sv[SPL], zv[SPL], sbv[XPL] = {}, zbv[XPL] = {};
+    float xv[XPL] = {};
 #pragma unroll
-        for (int i = 0; i < SPT; ++i) {
-            const int idx = base + i * SC::NT + tid;
-            const int is = min(idx, nsz - 1);
-            const int64_t src = (int64_t)min(r0 + is / G, R - 1) * G + is % G;
-            sv[i] = p.wscale[src];
-            zv[i] = p.wzero[src];
+    for (int i = 0; i < SPL; ++i) {
+        const int e = min(lane + 64 * i, ROWS * NG - 1), row = e / NG, gj = min(e % NG, ngs - 1);
+        const int64_t src = (int64_t)min(r0 + row, R - 1) * G + gs0 + gj;
+        sv[i] = p.wscale[src];
+        zv[i] = p.wzero[src];
+    }
+    if constexpr (XS) {
+#pragma unroll
+        for (int i = 0; i < XPL; ++i) {
+            const int e = min(lane + 64 * i, 16 * XF * NG - 1), gj = min(e / (16 * XF), ngs - 1), c = e % (16 * XF);
             if constexpr (RAWB) {
-                // sB and zB (converted, and zeroed past N, at the store: a
-                // use here would wait for the load before the stream goes out)
-                const int e = min(max(idx - nsz, 0), nxs - 1), g = e / 16, c = e % 16;
-                const int64_t si = (int64_t)g * p.N + min(c, p.N - 1);
+                // sB and zB (converted, and zeroed past N, at the store: a use
+                // here would wait for the load before the stream goes out)
+                const int64_t si = (int64_t)(gs0 + gj) * p.N + min(c, p.N - 1);
                 sbv[i] = p.bscale[si];
                 zbv[i] = p.bzero[si];
-            } else if constexpr (XS) {
-                const int e = min(max(idx - nsz, 0), nxs - 1), g = e / (16 * XF), c = e % (16 * XF);
-                xv[i] = p.xs[(int64_t)g * p.ldxs + c];
+            } else {
+                xv[i] = p.xs[(int64_t)(gs0 + gj) * p.ldxs + c];
             }
         }
-    };
-    auto stage_store = [&](int base) {
-#pragma unroll
-        for (int i = 0; i < SPT; ++i) {
-            const int idx = base + i * SC::NT + tid;
-            if (idx < nsz) {
-                lds_s[idx] = sv[i];
-                lds_z[idx] = zv[i];
-            } else if (XS && idx < nsz + nxs) {
-                if constexpr (RAWB) {
-                    const bool in = (idx - nsz) % 16 < p.N;
-                    lds_xs[idx - nsz] = in ? h2f(sbv[i]) : 0.0f;
-                    lds_zb[idx - nsz] = in ? zbv[i] : (uint16_t)0;
-                } else {
-                    lds_xs[idx - nsz] = xv[i];
-                }
-            }
-        }
-    };
-    stage_load(0);
+    }
     __builtin_amdgcn_sched_barrier(0);  // (keep the order: staging loads, then the stream)
 #pragma unroll
     for (int j = 0; j < D; ++j) issue(slot[j], j);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (RAWB) {
-        // this wave's groups of B to LDS, then from k-row order to step order.
-        // In group g, lane l's 16 bytes (rows 2 l, 2 l + 1) go to slot
-        // (l + g) % 64.  Unit u = (group, h, half d) reads dword d (columns
-        // 8 d .. 8 d + 7, column c at nibble c ^ 1) of the rows
-        // k = 32 q + 8 h + r, r < 8, q < 4, of its group and writes column
-        // col = 8 d + c's dword of step q to word q of slot 16 h + (col + g) % 16.
-        // The rotations by g spread the lanes of every access over the banks:
-        // two lanes a bank for the reads, the minimum four passes for the
-        // 16-byte writes, and the steps' reads stay one slot a lane.  Only the
-        // wave that owns a group touches it here, and one wave's LDS accesses
-        // take effect in program order: its copy lands before its reads, and
-        // its reads (each write needs all 32 of its lane's reads) before its
-        // writes.  The barrier below orders the reorder before the steps.
+        // this wave's groups of B to LDS in k-row order, 8 bytes a row, with
+        // the two 16-row halves of every odd 32-row block swapped (lane l's 16
+        // bytes are rows 2 l and 2 l + 1; chunk l goes to chunk l ^ 8 when bit
+        // 4 of l is set): a transposing read of lane group h covers 16 rows of
+        // block h, and with the swap the four lane groups of one read fall on
+        // alternate 128-byte halves of the banks (two passes, the minimum for
+        // 512 bytes)
 #pragma unroll
         for (int j = 0; j < NG; ++j)
-            if (g0 + j < g1)
-                *reinterpret_cast<u32x4*>(lds_b + (g0 + j) * 1024 + ((lane + g0 + j) & 63) * 16) = braw[j];
-        for (int u = lane; u < 8 * (g1 - g0); u += 64) {
-            const int g = g0 + (u >> 3), hh = (u >> 1) & 3, d = u & 1;
-            unsigned char* gb = lds_b + g * 1024;
-            unsigned y[4][8];
+            if (j < ngs)
+                *reinterpret_cast<u32x4*>(lds_b + (gs0 + j) * 1024 + (lane ^ (((lane >> 4) & 1) << 3)) * 16) = braw[j];
+    }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                unsigned x[8];
-#pragma unroll
-                for (int r = 0; r < 8; ++r)
-                    x[r ^ 1] = *reinterpret_cast<const unsigned*>(
-                        gb + ((16 * q + 4 * hh + (r >> 1) + g) & 63) * 16 + 8 * (r & 1) + 4 * d);
-                nibble_transpose8(x);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) y[q][c] = x[c ^ 1];
-            }
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                *reinterpret_cast<u32x4*>(gb + (16 * hh + ((8 * d + c + g) & 15)) * 16) =
-                    u32x4{y[0][c], y[1][c], y[2][c], y[3][c]};
+    for (int i = 0; i < SPL; ++i) {
+        const int e = lane + 64 * i, row = e / NG, gj = e % NG;
+        if (e < ROWS * NG && gj < ngs) {
+            lds_s[row * G + gs0 + gj] = sv[i];
+            lds_z[row * G + gs0 + gj] = zv[i];
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
-    stage_store(0);
-    // (more than SPT elements per thread: rare, and those loads wait behind the stream)
-    for (int base = SPT * SC::NT; base < nsz + nxs; base += SPT * SC::NT) {
-        stage_load(base);
-        stage_store(base);
+    if constexpr (XS) {
+#pragma unroll
+        for (int i = 0; i < XPL; ++i) {
+            const int e = lane + 64 * i, gj = e / (16 * XF), c = e % (16 * XF);
+            if (e < 16 * XF * NG && gj < ngs) {
+                const int d = (gs0 + gj) * 16 * XF + c;
+                if constexpr (RAWB) {
+                    const bool in = c < p.N;
+                    lds_xs[d] = in ? h2f(sbv[i]) : 0.0f;
+                    lds_zb[d] = in ? zbv[i] : (uint16_t)0;
+                } else {
+                    lds_xs[d] = xv[i];
+                }
+            }
+        }
     }
-    __syncthreads();
+    const unsigned lds_b_addr = (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char*)lds_b);
+    // (the K loop's LDS reads stay behind these stores)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
     f32x4 acc[XF][WF];
 #pragma unroll
@@ -286,15 +256,22 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
             }
             if constexpr (XS) {
 #pragma unroll
-                for (int x = 0; x < XF; ++x)
-                    c.sx[x] = *reinterpret_cast<const f32x4*>(lds_xs + g * 16 * XF + 16 * x + 4 * h);
+                for (int x = 0; x < XF; ++x) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(lds_xs + g * 16 * XF + 16 * x + 4 * h);
+                    // raw B: accumulator row 4 h + e is column 4 h + (e ^ 1)
+                    c.sx[x] = RAWB ? f32x4{v[1], v[0], v[3], v[2]} : v;
+                }
             }
             if constexpr (RAWB) {
-                c.zb = lds_zb[g * 16 + l16];
-                // column l16, rows k = 128 g + 32 q + 8 h .. + 7 in word q, packed
-                // as the weights are (byte j: row 2j high, row 2j + 1 low), in
-                // slot 16 h + (l16 + g) % 16
-                c.bq = *reinterpret_cast<const u32x4*>(lds_b + g * 1024 + (16 * h + ((l16 + g) & 15)) * 16);
+                c.zb = lds_zb[g * 16 + (l16 ^ 1)];
+                // column l16 ^ 1, rows k = 128 g + 32 h + 8 q .. + 7 in word q
+                // (two transposing reads of 16 rows; odd blocks h have their
+                // halves swapped, see the copy above)
+                const unsigned gb = lds_b_addr + g * 1024;
+                const int sw = (h & 1) << 4;
+                const u32x2 lo = lds_read_tr4(gb + 8 * ((32 * h + l16) ^ sw));
+                const u32x2 hi = lds_read_tr4(gb + 8 * ((32 * h + 16 + l16) ^ sw));
+                c.bq = u32x4{lo.x, lo.y, hi.x, hi.y};
             }
             return c;
         };
@@ -305,7 +282,8 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
             f16x2 zz[WF];
 #pragma unroll
             for (int f = 0; f < WF; ++f) {
-                wt[f] = transpose_lane_groups(s.w[f]);
+                // (raw B takes the k order in which the slices arrive)
+                wt[f] = RAWB ? s.w[f] : transpose_lane_groups(s.w[f]);
                 const _Float16 nz = (_Float16)(-rintf(h2f(c.z[f])) * (1.0f / 512.0f));
                 zz[f] = f16x2{nz, nz};
             }
@@ -318,7 +296,7 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
             for (int q = 0; q < 4; ++q) {
                 f16x8 xq[XF];
                 if constexpr (RAWB) {
-                    xq[0] = unpack8(q == 0 ? c.bq.x : q == 1 ? c.bq.y : q == 2 ? c.bq.z : c.bq.w, zzb);
+                    xq[0] = unpack8<true>(q == 0 ? c.bq.x : q == 1 ? c.bq.y : q == 2 ? c.bq.z : c.bq.w, zzb);
                 } else {
 #pragma unroll
                     for (int x = 0; x < XF; ++x) xq[x] = s.x[x][q];
@@ -425,14 +403,16 @@ __global__ void __launch_bounds__(SC::NT) i4w_stream(Args p) {
         for (int x = 0; x < XF; ++x) {
             const int c = 16 * x + 4 * h;
             if constexpr (OUT == 0) {
+                // (raw B: accumulator entry e is column c + (e ^ 1))
+                constexpr int SW = RAWB ? 1 : 0;
                 uint16_t* dst = p.out + (int64_t)r * p.C + c;
                 if (c + 3 < p.C && (p.C & 3) == 0) {
-                    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(acc[x][f][0], acc[x][f][1]),
-                                                           pack2h(acc[x][f][2], acc[x][f][3])};
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{pack2h(acc[x][f][0 ^ SW], acc[x][f][1 ^ SW]),
+                                                           pack2h(acc[x][f][2 ^ SW], acc[x][f][3 ^ SW])};
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (c + e < p.C) dst[e] = f2h(acc[x][f][e]);
+                        if (c + e < p.C) dst[e] = f2h(acc[x][f][e ^ SW]);
                 }
             } else {
 #pragma unroll
