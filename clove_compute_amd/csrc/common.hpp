@@ -189,11 +189,15 @@ __device__ __forceinline__ void splitk_publish(float* slab, int tid, const f32x4
 }
 
 // slabs: the nsplit consecutive slabs of one tile; INT sums int32 lanes.
+// `sum` holds the caller's own partial (the one it published as split `own`)
+// on entry and the total on return; the own slab is not read back (SKIP_OWN,
+// for up to 32 chunks per thread: beyond that the copy of the own partial
+// would not fit the registers of the kernels that use it).
 // Chunks are reduced 16 at a time (bounded registers); within a chunk group
 // the loads of SB splits (up to 32 loads) are in flight together, so a small
 // tile needs one round trip to the coherent level for all of its splits.
-template <int NC, int NT, bool INT>
-__device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, int tid, f32x4 (&sum)[NC]) {
+template <int NC, int NT, bool INT, bool SKIP_OWN = (NC <= 32)>
+__device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, int own, int tid, f32x4 (&sum)[NC]) {
     constexpr int CG = NC < 16 ? NC : 16;
     constexpr int SB = 32 / CG > 1 ? 32 / CG : 1;
     static_assert(NC % CG == 0, "chunk groups");
@@ -201,11 +205,23 @@ __device__ __forceinline__ void splitk_reduce(const float* slabs, int nsplit, in
         const_cast<float*>(slabs), (short)0, nsplit * NC * NT * 16, 0x00020000);
 #pragma unroll
     for (int c0 = 0; c0 < NC; c0 += CG) {
+        f32x4 mine[SKIP_OWN ? CG : 1];
+        if constexpr (SKIP_OWN) {
+#pragma unroll
+            for (int c = 0; c < CG; ++c) mine[c] = sum[c0 + c];
+        }
         for (int s0 = 0; s0 < nsplit; s0 += SB) {
             f32x4 buf[SB][CG];
 #pragma unroll
             for (int b = 0; b < SB; ++b) {
                 if (s0 + b >= nsplit) break;  // uniform: no loads past the last split
+                if constexpr (SKIP_OWN) {
+                    if (s0 + b == own) {  // uniform: the own partial is in registers
+#pragma unroll
+                        for (int c = 0; c < CG; ++c) buf[b][c] = mine[c];
+                        continue;
+                    }
+                }
 #pragma unroll
                 for (int c = 0; c < CG; ++c)
                     buf[b][c] = bitcast<f32x4>(__builtin_amdgcn_raw_buffer_load_b128(

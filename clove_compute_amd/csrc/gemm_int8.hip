@@ -262,7 +262,7 @@ __global__ void __launch_bounds__(WGM* WGN * 64) int8_mfma(I8Params p) {
                                                                    acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
         splitk_publish<NC, NT>(slabs + (int64_t)tc.split * (BM * BN), tid, v);
         if (!splitk_arrive_is_last(&p.counters[tile_id], (unsigned)p.nsplit, &s_last)) return;
-        splitk_reduce<NC, NT, true>(slabs, p.nsplit, tid, v);
+        splitk_reduce<NC, NT, true>(slabs, p.nsplit, tc.split, tid, v);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll

@@ -576,7 +576,7 @@ __global__ void __launch_bounds__(NT) i4i4_gemm(Args p) {
         if (set == 0) splitk_publish<NC, 256>(slabs + (size_t)split * NC * 256 * 4, tid, v);
         if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
             return;
-        if (set == 0) splitk_reduce<NC, 256, false>(slabs, p.nsplit, tid, v);
+        if (set == 0) splitk_reduce<NC, 256, false>(slabs, p.nsplit, split, tid, v);
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll

@@ -400,7 +400,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
         // the stages are dead here (every DMA was waited for, every read returned)
         if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
             return;
-        splitk_reduce<NC, CF::NT, false>(slabs, p.nsplit, tid, v);
+        splitk_reduce<NC, CF::NT, false>(slabs, p.nsplit, split, tid, v);
 #pragma unroll
         for (int i = 0; i < FW; ++i)
 #pragma unroll

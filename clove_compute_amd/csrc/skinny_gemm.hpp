@@ -311,7 +311,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
         splitk_publish<NC, CF::NT>(slabs + (size_t)split * NC * CF::NT * 4, tid, v);
         if (!splitk_arrive_is_last(p.counters + tile, (unsigned)p.nsplit, reinterpret_cast<int*>(smem)))
             return;
-        splitk_reduce<NC, CF::NT, I8>(slabs, p.nsplit, tid, v);
+        splitk_reduce<NC, CF::NT, I8>(slabs, p.nsplit, split, tid, v);
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
