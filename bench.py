@@ -861,7 +861,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the GEMM path has no "
-              "multi-GPU component in this build. Run with --gpus 1.", file=sys.stderr)
+              "multi-GPU component (each call runs on one GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
