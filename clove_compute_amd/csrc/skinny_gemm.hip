@@ -24,6 +24,16 @@ using F16T64 = Cfg<false, 64, 64, 2, 2, 6>;
 // 5.5 -> 4.7 us; from K = 1024 the six stages are ahead, 1024^3 8.7 against
 // 13.2 us)
 using F16T64S2 = Cfg<false, 64, 64, 2, 2, 2>;
+// small products (short K, at most one 32x32 tile per CU): 32x32 tiles whose
+// four waves take one k-step of every K tile each, two stages ahead -- 4x the
+// workgroups of 64x64 tiles at a quarter of the operand bytes each (hot graph
+// replays, us per call, against the 64x64 / 32x128 tiles: 512^3 4.98 / 5.61
+// -> 4.27, 512 x 512 x 1024 6.90 / 7.83 -> 5.51, 64 x 4096 x 1024 6.91 / 7.83
+// -> 5.49, 3 x 8192 x 1024 6.72 / 7.71 -> 5.33, 100 x 200 x 320 4.04 / 4.53
+// -> 3.67; one or three stages ahead no faster; at 512 such tiles and more it
+// only ties or loses: 512 x 1024 x 512 5.27 -> 5.21, 1024 x 1024 x 512 5.81
+// -> 7.13)
+using F16K32 = Cfg<false, 32, 32, 1, 1, 3, 1, 4>;
 using I8M32 = Cfg<true, 32, 128, 1, 4, 5>;
 using I8M128 = Cfg<true, 128, 64, 4, 1, 4>;
 using I8T128 = Cfg<true, 128, 128, 2, 2, 3>;
@@ -41,7 +51,7 @@ clove_status_t run(Args a, int batch, int cus, hipStream_t stream) {
     // (512^3: 8.4 us with 4 splits, 7.2 us with none, measured)
     int ns = tiles >= cus ? 1 : cus / tiles;
     ns = max(1, min(ns, nk / 2));
-    if (nk <= 16) ns = 1;
+    if (nk <= 16 || CF::KW > 1) ns = 1;
     const int kt_per = cdiv(nk, ns);
     a.kps = kt_per * CF::BK;
     a.nsplit = cdiv(nk, kt_per);
@@ -65,11 +75,12 @@ bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 31); }
 // The FP16 tile shapes, chosen by shape alone (so that the fused SwiGLU below
 // picks the same tiles, and with them the same split plan, as the two GEMMs
 // it replaces).
-enum class F16Tile { kM32, kM128, kT128, kT64 };
+enum class F16Tile { kM32, kM128, kT128, kT64, kK32 };
 
 F16Tile pick_f16_tile(int batch, int M, int N, int K, int cus) {
     const bool short_k = K <= 16 * F16M128::BK;  // no split K (see run)
     const bool long_k = K >= 4096;
+    if (short_k && (int64_t)cdiv(M, F16K32::BM) * cdiv(N, F16K32::BN) * batch <= cus) return F16Tile::kK32;
     // 128x128 tiles, split K when they are few: for M > 256 once they cover
     // half the CUs or K is long, for 128 < M <= 256 on long K and N >= 4096
     // (cold weights, against 64x64 tiles for M > 256 and 128x64 up to 256:
@@ -113,6 +124,7 @@ using SwM32 = Cfg<false, 32, 128, 1, 4, 4, 2>;
 using SwM128 = Cfg<false, 128, 64, 4, 1, 4, 2>;
 using SwT128 = Cfg<false, 128, 128, 2, 2, 3, 2>;
 using SwT64 = Cfg<false, 64, 64, 2, 2, 6, 2>;
+using SwK32 = Cfg<false, 32, 32, 1, 1, 3, 2, 4>;
 
 }  // namespace
 
@@ -139,6 +151,7 @@ bool try_skinny_fp16(const uint16_t* A, const uint16_t* B, uint16_t* C, int batc
             *status = K <= 512 ? run<F16T64S2, kF16AlphaBeta>(a, batch, cus, stream)
                                : run<F16T64, kF16AlphaBeta>(a, batch, cus, stream);
             break;
+        case F16Tile::kK32: *status = run<F16K32, kF16AlphaBeta>(a, batch, cus, stream); break;
     }
     return true;
 }
@@ -163,6 +176,7 @@ bool try_skinny_swiglu(const uint16_t* X, const uint16_t* W_gate, const uint16_t
         case F16Tile::kM128: *status = run<SwM128, kF16SwiGLU>(a, 1, cus, stream); break;
         case F16Tile::kT128: *status = run<SwT128, kF16SwiGLU>(a, 1, cus, stream); break;
         case F16Tile::kT64: *status = run<SwT64, kF16SwiGLU>(a, 1, cus, stream); break;
+        case F16Tile::kK32: *status = run<SwK32, kF16SwiGLU>(a, 1, cus, stream); break;
     }
     return true;
 }

@@ -64,12 +64,17 @@ struct Args {
     unsigned* counters;
 };
 
-template <bool I8_, int BM_, int BN_, int WM_, int WN_, int S_, int NB_ = 1>
+// KW > 1: KW waves share each wave tile and take disjoint slices of every K
+// tile's four k-steps, summed through LDS after the K loop (slice order, so
+// deterministic): KW times the workgroups of the same wave tiles for small
+// products (no split K)
+template <bool I8_, int BM_, int BN_, int WM_, int WN_, int S_, int NB_ = 1, int KW_ = 1>
 struct Cfg {
     static constexpr bool I8 = I8_;
-    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, S = S_, NB = NB_;
+    static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, S = S_, NB = NB_, KW = KW_;
     static constexpr int ES = I8 ? 1 : 2;  // bytes per element
-    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int NW = WM * WN * KW, NT = 64 * NW;
+    static constexpr int NKS = 4 / KW;     // k-steps per K tile per wave
     static constexpr int BK = 128 / ES;    // K per stage: 128 bytes of every A row
     static constexpr int BNB = BN * ES;    // bytes of one B k-row in the tile
     static constexpr int FM = BM / (32 * WM), FN = BN / (32 * WN);
@@ -82,8 +87,11 @@ struct Cfg {
     static_assert(FM >= 1 && FN >= 1 && BM == 32 * FM * WM && BN == 32 * FN * WN, "wave tiles");
     static_assert(BNB == 64 || BNB == 128 || BNB == 256 || BNB == 512, "B row bytes");
     static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "DMA split");
-    static_assert(S >= 2 && S <= 6 && (S - 2) * D <= 63, "stages");
-    static constexpr int LDS = S * SB;
+    static_assert(S >= 2 && S <= 9 && (S - 2) * D <= 63, "stages");
+    static_assert(KW == 1 || ((KW == 2 || KW == 4) && !I8), "k slices");
+    // the k-slice sums: every wave's NB FN FM 32x32 blocks, 4 KB each
+    static constexpr int RED = KW > 1 ? NW * NB * FN * FM * 4096 : 0;
+    static constexpr int LDS = S * SB + RED;
     static_assert(LDS <= 160 * 1024, "LDS");
 };
 
@@ -118,19 +126,18 @@ __device__ __forceinline__ u32x2 lds_read_tr(unsigned a) {
 
 // wait until stage t has landed, `ahead` later stages may stay in flight,
 // then the workgroup barrier
-template <int S, int D>
+// (ahead <= S - 2)
+template <int S, int D, int A = S - 2>
 __device__ __forceinline__ void stage_wait(int ahead) {
-    if constexpr (S >= 6) {
-        if (ahead >= 4) { dma::stage_barrier<vmcnt_imm(4 * D)>(); return; }
+    if constexpr (A >= 1) {
+        if (ahead >= A) {
+            dma::stage_barrier<vmcnt_imm(A * D)>();
+            return;
+        }
+        stage_wait<S, D, A - 1>(ahead);
+    } else {
+        dma::stage_barrier<vmcnt_imm(0)>();
     }
-    if constexpr (S >= 5) {
-        if (ahead >= 3) { dma::stage_barrier<vmcnt_imm(3 * D)>(); return; }
-    }
-    if constexpr (S >= 4) {
-        if (ahead >= 2) { dma::stage_barrier<vmcnt_imm(2 * D)>(); return; }
-    }
-    if (ahead >= 1) dma::stage_barrier<vmcnt_imm(D)>();
-    else dma::stage_barrier<vmcnt_imm(0)>();
 }
 
 template <class CF, int OUT>
@@ -143,7 +150,10 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave % CF::WM, wn = wave / CF::WM;
+    const int kw = wave / (CF::WM * CF::WN);  // k slice (0 unless KW > 1)
+    const int wmn = wave - kw * (CF::WM * CF::WN);
+    const int wm = wmn % CF::WM, wn = wmn / CF::WM;
+    constexpr int NKS = CF::NKS;
 
     // ---- tile, split, K range ----
     // Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD
@@ -213,10 +223,14 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
 
     // ---- fragment addressing (relative to the stage) ----
     const int kh = lane >> 5, l32 = lane & 31;
-    // A: row wm*32FM + 32j + l32, k-step t reads chunk (2t + kh) ^ (l & 7); tile j is +4096 j
-    unsigned aoff[4];
+    // A: row wm*32FM + 32j + l32, k-step t reads chunk (2t + kh) ^ (l & 7); tile j is +4096 j.
+    // The wave's k-steps of a K tile are t = NKS kw + u, u < NKS.
+    unsigned aoff[NKS];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) aoff[t] = (wm * 32 * FM + l32) * 128 + 16 * ((2 * t + kh) ^ (lane & 7));
+    for (int u = 0; u < NKS; ++u) {
+        const int t = NKS * kw + u;
+        aoff[u] = (wm * 32 * FM + l32) * 128 + 16 * ((2 * t + kh) ^ (lane & 7));
+    }
     // B: group g = l32 / 16 covers columns wn*32FN + 32i + 16g .. +15; source lane s = lane & 15
     // points at k-row (step rows) + s / RL and byte 8 (s % LR) of the group's columns
     constexpr int RL = I8 ? 2 : 4;        // lanes per k-row in one transposing read
@@ -224,16 +238,17 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
     const int s16 = lane & 15, g = l32 >> 4;
     // (the swizzle mixes chunk bits that distinguish the tiles i, so every
     // tile has its own offsets)
-    unsigned boff[4][2][FN];              // [k-step][read][tile]
+    unsigned boff[NKS][2][FN];            // [k-step][read][tile]
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int u = 0; u < NKS; ++u)
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
             for (int i = 0; i < FN; ++i) {
+                const int t = NKS * kw + u;
                 const int row = t * (32 / ES) + kh * (16 / ES) + e * RR + s16 / RL;
                 const int col = (wn * 32 * FN + 32 * i + 16 * g) * ES + 8 * (s16 % RL);
-                boff[t][e][i] = CF::A_BYTES + row * BNB + 16 * ((col >> 4) ^ swz_b<BNB, I8>(row)) + (col & 15);
+                boff[u][e][i] = CF::A_BYTES + row * BNB + 16 * ((col >> 4) ^ swz_b<BNB, I8>(row)) + (col & 15);
             }
 
     typedef typename std::conditional<I8, i32x16, f32x16>::type AccT;
@@ -263,7 +278,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
         stage = stage + 1 == S ? 0 : stage + 1;
 
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < NKS; ++ks) {
             u32x4 af[FM];
             const unsigned ab = st + aoff[ks];
 #pragma unroll
@@ -292,8 +307,52 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
         }
     }
 
-    // ---- split-K ----
-    if (p.nsplit > 1) {
+    // ---- k slices: every wave stores its sums to LDS; wave kw then owns the
+    // runs q with q / (4 / KW) == kw of every block and adds the KW slices in
+    // slice order ----
+    constexpr int NQ = 4 / CF::KW;  // runs of 4 columns per block owned by a wave
+    if constexpr (CF::KW > 1) {
+        const unsigned red = lds0 + (unsigned)(S * SB);
+        // wave tile wmn, slice s, block (b, i, j), run q: 1 KB, 16 lane-contiguous
+        // bytes per lane
+        auto slot = [&](int s, int b, int i, int j, int q) {
+            return red +
+                   (unsigned)(((((((wmn * CF::KW + s) * NB + b) * FN + i) * FM + j) * 4 + q) << 10) + 16 * lane);
+        };
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<lds_u32x4*>((size_t)slot(kw, b, i, j, q)) = bitcast<u32x4>(
+                            f32x4{acc[b][i][j][4 * q], acc[b][i][j][4 * q + 1], acc[b][i][j][4 * q + 2],
+                                  acc[b][i][j][4 * q + 3]});
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (q / NQ != kw) continue;
+                        f32x4 sum = bitcast<f32x4>(lds_read16(slot(0, b, i, j, q)));
+#pragma unroll
+                        for (int s = 1; s < CF::KW; ++s) {
+                            const f32x4 v = bitcast<f32x4>(lds_read16(slot(s, b, i, j, q)));
+                            sum = f32x4{sum[0] + v[0], sum[1] + v[1], sum[2] + v[2], sum[3] + v[3]};
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[b][i][j][4 * q + e] = sum[e];
+                    }
+    }
+
+    // ---- split-K (not with k slices: the host plans none) ----
+    if (CF::KW == 1 && p.nsplit > 1) {
         constexpr int NC = NB * FN * FM * 4;
         f32x4 v[NC];
 #pragma unroll
@@ -346,6 +405,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
                 for (int i = 0; i < FN; ++i)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
+                        if (CF::KW > 1 && q / NQ != kw) continue;
                         const int nc = min(n0 + wn * 32 * FN + 32 * i + 8 * q + 4 * kh, N - 4);
                         oldc[j][i][q] =
                             *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(Cb) + (int64_t)mc * N + nc);
@@ -372,6 +432,7 @@ __global__ void __launch_bounds__(CF::NT) skinny_gemm(Args p) {
         for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                if (CF::KW > 1 && q / NQ != kw) continue;
                 const int n = n0 + wn * 32 * FN + 32 * i + 8 * q + 4 * kh;
                 if (n >= N) continue;  // N % 8 == 0: the run is whole
                 if constexpr (OUT == kI8Acc32) {

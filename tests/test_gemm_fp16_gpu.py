@@ -272,8 +272,24 @@ def test_skinny_shapes(M, N, K):
     check_rows(A, B, C, rows, C0, 0.75, -0.5)
 
 
+# short K with at most one 32x32 tile per CU: 32x32 tiles whose four waves
+# each take one k-step of every K tile, the four sums added through LDS
+# (alpha / beta, ragged M and N, M = 3 on a weight that skips the GEMV)
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (64, 512, 1024), (3, 8192, 1024), (32, 4096, 512),
+                                   (100, 200, 320)])
+def test_k_sliced_small_tiles(M, N, K):
+    g = rng("k-sliced", M, N, K)
+    A = g.standard_normal((M, K)).astype(np.float16)
+    B = (g.standard_normal((K, N)) * 0.02).astype(np.float16)
+    C0 = g.standard_normal((M, N)).astype(np.float16)
+    C = run_fp16(A, B, C0, alpha=0.75, beta=-0.5)
+    rows = np.arange(M) if M <= 100 else np.unique(np.concatenate([[0, 31, 32, M - 1], g.integers(0, M, 24)]))
+    check_rows(A, B, C, rows, C0, 0.75, -0.5)
+
+
 @pytest.mark.parametrize("M,N,K", [(7, 4096, 4096), (100, 264, 640), (128, 4096, 4096),
-                                   (3, 4096, 4096), (2, 11008, 4096), (4, 4096, 11008)])
+                                   (3, 4096, 4096), (2, 11008, 4096), (4, 4096, 11008),
+                                   (512, 512, 1024), (3, 8192, 1024)])
 def test_skinny_small_integers_bit_exact(M, N, K):
     # |a|, |b| <= 4 integers: every product and partial sum is exact in fp32,
     # so split K and the fp16 output are exact (M = 2..4 on these weights
