@@ -8,8 +8,10 @@
 //
 //  * w4a16_gemv (T <= 2, and T = 3, 4 on small weights: decode) -- a wave
 //    streams one or more weight rows with 16-byte loads, all in flight at once; the nibbles are turned into the
-//    exact fp16 integers q - z and dotted with X (staged in LDS) by
-//    v_dot2_f32_f16 in fp32; acc += scale * that per 32-k chunk.
+//    exact fp16 integers q - z and dotted with X (staged in LDS, or for one
+//    token on rows of up to 2048 k loaded per lane into registers, where the
+//    zero point comes off once per chunk) by v_dot2_f32_f16 in fp32;
+//    acc += scale * that per 32-k chunk.
 //  * larger T -- the INT4-weight MFMA GEMM (i4w_gemm.hpp) when K % 128 == 0
 //    and the operands are aligned, else the shared MFMA GEMM (mfma_gemm.hpp):
 //    X rows as operand A, W rows unpacked to the exact integers q - z as
@@ -56,6 +58,15 @@ __host__ __device__ constexpr int xperm(int k) { return (k & ~7) | ((k & 1) << 2
 // q - z exactly, and v_dot2_f32_f16 with the X pairs accumulates
 // sum_k x_k (q_k - z) in fp32 with exact products; acc += s * that per chunk.
 //
+// DX (one token, one aligned chunk per lane, K % 32 == 0, 16-byte aligned X):
+// no LDS.  Each lane loads the 32 x of its own chunk straight into registers
+// (they serve every row of the wave), permutes them into the unpack order
+// there and sums them once (sx, fp32); the rows then dot x with 1024 + q and
+// subtract (1024 + z) * sx per chunk, which takes the per-weight zero-point
+// subtraction out of the inner loop.  The products are still exact; the fp32
+// sums carry the 1024 offset (relative to the chunk's sum of |x| the rounding
+// is ~2^-24 * 1039).  Integer-valued x and q - z stay exact below 2^24.
+//
 // SWIGLU: the weight holds 2 O rows (gate rows 0..O-1, then up rows O..2O-1)
 // and the output is H [T, O] = swiglu(fp16(gate), fp16(up)); a wave takes RPW/2
 // gate rows and the RPW/2 up rows of the same outputs, so the pair meets in
@@ -68,9 +79,10 @@ __host__ __device__ constexpr int w4_max_threads() {
     return (RPW >= 4 && UPR >= 2) ? 512 : gemv_max_threads<TV, ALIGNED, 2>();
 }
 
-template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false>
+template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false, bool DX = false>
 __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a16_gemv(GemvParams p) {
     static_assert(!SWIGLU || RPW % 2 == 0, "gate / up row pairs");
+    static_assert(!DX || (TV == 1 && UPR == 1 && ALIGNED && RPW <= 4), "direct X: one token, one chunk per lane");
     constexpr int LR = SWIGLU ? RPW / 2 : RPW;  // output rows per wave
     extern __shared__ __attribute__((aligned(16))) unsigned lds[];
     const int NT = blockDim.x, WPB = NT >> 6;  // waves per workgroup (rows / RPW)
@@ -89,10 +101,15 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
     // thread; with several tokens, any further pieces are loaded at the
     // staging -- one token always fits for K <= 32768) ----
     const int npieces = TV * KP / 8;
-    const bool xfast = (TV > 1 || npieces <= XPT * NT) && (K & 7) == 0 &&
+    const bool xfast = !DX && (TV > 1 || npieces <= XPT * NT) && (K & 7) == 0 &&
                        (reinterpret_cast<uintptr_t>(p.X) & 15) == 0;
     u32x4 xr[XPT];
-    if (xfast) {
+    if constexpr (DX) {
+        // the lane's chunk (nch <= 64: lanes past the end reload the last one)
+        const int cs = min(lane, nch - 1);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xr[d] = *reinterpret_cast<const u32x4*>(p.X + 32 * cs + 8 * d);
+    } else if (xfast) {
 #pragma unroll
         for (int i = 0; i < XPT; ++i) {
             const int q = min(tid + i * NT, npieces - 1);
@@ -138,7 +155,8 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
     load_batch(0);
 
     // ---- stage X in the permuted order ----
-    if (xfast) {
+    if constexpr (DX) {
+    } else if (xfast) {
 #pragma unroll
         for (int i = 0; i < XPT; ++i) {
             const int q = tid + i * NT;
@@ -169,7 +187,23 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
             Xs[t * KP + xperm(k)] = (t < p.T && k < K) ? p.X[(int64_t)t * K + k] : (uint16_t)0;
         }
     }
-    lds_barrier();
+    if constexpr (!DX) lds_barrier();
+    // DX: the lane's x in the unpack order, and their sum
+    u32x4 xd[4];
+    float sx = 0.0f;
+    if constexpr (DX) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const u32x4 v = xr[d];
+            xd[d] = u32x4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                          __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+            sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].x), one, sx, false);
+            sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].y), one, sx, false);
+            sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].z), one, sx, false);
+            sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].w), one, sx, false);
+        }
+    }
 
     float acc[RPW][TV];
 #pragma unroll
@@ -190,15 +224,23 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
                 const bool valid = row0 + r % LR < p.O && c < nch;
                 const float sc = valid ? h2f(sh[r][u]) : 0.0f;
                 const f16x2 zz = mg::magic_zero(zh[r][u]);
+                // (DX: 1024 + q; the zero point comes off per chunk below)
                 f16x2 qz[16];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     const unsigned w = a[r][u][d];
                     const unsigned hi = (w >> 4) & 0x0f0f0f0fu, lo = w & 0x0f0f0f0fu;
-                    qz[4 * d + 0] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04010400u)) - zz;
-                    qz[4 * d + 1] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04030402u)) - zz;
-                    qz[4 * d + 2] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04010400u)) - zz;
-                    qz[4 * d + 3] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04030402u)) - zz;
+                    if constexpr (DX) {
+                        qz[4 * d + 0] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04010400u));
+                        qz[4 * d + 1] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04030402u));
+                        qz[4 * d + 2] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04010400u));
+                        qz[4 * d + 3] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04030402u));
+                    } else {
+                        qz[4 * d + 0] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04010400u)) - zz;
+                        qz[4 * d + 1] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04030402u)) - zz;
+                        qz[4 * d + 2] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04010400u)) - zz;
+                        qz[4 * d + 3] = bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04030402u)) - zz;
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < TV; ++t) {
@@ -206,12 +248,13 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
                     float dot = 0.0f;
 #pragma unroll
                     for (int d = 0; d < 4; ++d) {
-                        const u32x4 x = xv[d];
+                        const u32x4 x = DX ? xd[d] : xv[d];
                         dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.x), qz[4 * d + 0], dot, false);
                         dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.y), qz[4 * d + 1], dot, false);
                         dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.z), qz[4 * d + 2], dot, false);
                         dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(x.w), qz[4 * d + 3], dot, false);
                     }
+                    if constexpr (DX) dot = fmaf(-static_cast<float>(zz[0]), sx, dot);
                     acc[r][t] = fmaf(sc, dot, acc[r][t]);
                 }
             }
@@ -293,12 +336,20 @@ inline GemvShape gemv_shape(int rows, int nch, int cus, int wg_min = 1) {
     return g;
 }
 
+// DX (X straight into registers, no LDS) wherever it applies: one token, one
+// aligned chunk per lane, aligned X (cold graph replays, us per call: Llama-1B
+// decode QKV 3072 x 2048 3.62 -> 3.44, O 2048 x 2048 3.44 -> 3.36, gate/up +
+// SwiGLU 2 x 8192 x 2048 6.80 -> 6.08; down 2048 x 8192, four chunks per lane,
+// measured slower with X in registers, 5.31 -> 5.84, and keeps the LDS)
 template <int TV, int RPW, int UPR, bool ALIGNED, bool SWIGLU = false>
 clove_status_t run_gemv_shape(const GemvParams& p, int wpb, hipStream_t stream) {
-    const size_t lds = gemv_lds_bytes(TV, p.nch);
+    // (not with eight rows per wave: their weights and x do not fit the VGPRs)
+    constexpr bool DXOK = TV == 1 && UPR == 1 && ALIGNED && RPW <= 4;
+    const bool dx = DXOK && p.nch <= 64 && aligned16(p.X);
+    const size_t lds = dx ? 0 : gemv_lds_bytes(TV, p.nch);
     wpb = min(wpb, w4_max_threads<TV, RPW, UPR, ALIGNED>() / 64);
     const dim3 grid(cdiv(p.O, wpb * (SWIGLU ? RPW / 2 : RPW)));
-    auto k = w4a16_gemv<TV, RPW, UPR, ALIGNED, SWIGLU>;
+    auto k = dx ? w4a16_gemv<TV, RPW, UPR, ALIGNED, SWIGLU, DXOK> : w4a16_gemv<TV, RPW, UPR, ALIGNED, SWIGLU>;
     if (ensure_lds(reinterpret_cast<const void*>(k), (int)lds) != CLOVE_OK) return CLOVE_ERR_LAUNCH;
     CLOVE_LAUNCH(k, grid, dim3(wpb * 64), lds, stream, p);
     return check_launch();
