@@ -305,6 +305,94 @@ __global__ void __launch_bounds__((w4_max_threads<TV, RPW, UPR, ALIGNED>())) w4a
     }
 }
 
+// One token on longer rows (65 to 512 chunks: K % 32 == 0, aligned W and X):
+// the KS = ceil(nch / 64) waves of a workgroup share RPW rows and split K,
+// wave w taking chunk 64 w + lane of every row, its x straight into
+// registers and the zero point taken out per chunk as in DX; each wave sums
+// its lanes (the fixed butterfly), then wave 0 adds the KS partials of each
+// row in wave order.  X is read once per workgroup and never staged, and its
+// permute and sum serve RPW rows.  Cold graph replays, us per call, against
+// the row-per-wave GEMV with X staged in LDS: 2048 x 8192 (Llama-1B down)
+// 5.48 -> 4.68, 4096 x 4096 5.13 -> 4.65, 11008 x 4096 8.60 -> 7.17, 4096 x
+// 11008 9.32 -> 7.80, 14336 x 4096 9.88 -> 8.50, 8192 x 8192 12.05 -> 9.37,
+// 2048 x 16384 20.70 -> 6.59; four rows per workgroup ahead of two and one
+// (11008 x 4096: 7.24 / 8.05 / 10.39) wherever they still give two workgroups
+// per CU.
+template <int RPW>
+__global__ void __launch_bounds__(512) w4a16_gemv_ks(GemvParams p) {
+    __shared__ float part[8][RPW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int KS = blockDim.x >> 6;
+    const int nch = p.nch, K = p.K, G = p.G;
+    const int row0 = blockIdx.x * RPW;
+    const int c = wave * 64 + lane;
+    const int cs = min(c, nch - 1);  // lanes past the end: garbage, masked by s = 0
+    u32x4 xr[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) xr[d] = *reinterpret_cast<const u32x4*>(p.X + 32 * cs + 8 * d);
+    u32x4 a[RPW];
+    uint16_t sh[RPW], zh[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = min(row0 + r, p.O - 1);
+        a[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.W + (int64_t)row * (K / 2) + 16 * cs));
+        const int64_t gi = (int64_t)row * G + (cs >> 2);
+        sh[r] = p.scale[gi];
+        zh[r] = p.zero[gi];
+    }
+    // x in the unpack order (x0 x2)(x4 x6)(x1 x3)(x5 x7) per 8 k, and their sum
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    u32x4 xd[4];
+    float sx = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const u32x4 v = xr[d];
+        xd[d] = u32x4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                      __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+        sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].x), one, sx, false);
+        sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].y), one, sx, false);
+        sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].z), one, sx, false);
+        sx = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].w), one, sx, false);
+    }
+    constexpr unsigned C64 = 0x64646464u;
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const bool valid = row0 + r < p.O && c < nch;
+        const float sc = valid ? h2f(sh[r]) : 0.0f;
+        const f16x2 zz = mg::magic_zero(zh[r]);
+        float dot = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const unsigned w = a[r][d];
+            const unsigned hi = (w >> 4) & 0x0f0f0f0fu, lo = w & 0x0f0f0f0fu;
+            dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].x), bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04010400u)),
+                                         dot, false);
+            dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].y), bitcast<f16x2>(__builtin_amdgcn_perm(C64, hi, 0x04030402u)),
+                                         dot, false);
+            dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].z), bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04010400u)),
+                                         dot, false);
+            dot = __builtin_amdgcn_fdot2(bitcast<f16x2>(xd[d].w), bitcast<f16x2>(__builtin_amdgcn_perm(C64, lo, 0x04030402u)),
+                                         dot, false);
+        }
+        dot = fmaf(-static_cast<float>(zz[0]), sx, dot);
+        acc[r] = wave_sum(sc * dot);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) part[wave][r] = acc[r];
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= RPW) return;
+    float v = part[0][lane];
+    for (int w = 1; w < KS; ++w) v += part[w][lane];
+    const int row = row0 + lane;
+    if (row >= p.O) return;
+    float y = p.alpha * v;
+    if (p.beta != 0.0f) y = fmaf(p.beta, h2f(p.Y[row]), y);
+    p.Y[row] = f2h(y);
+}
+
 namespace {
 
 constexpr size_t kMaxGemvLds = 150 * 1024;
@@ -379,8 +467,25 @@ clove_status_t run_gemv_swiglu(const GemvParams& p, bool aligned, int cus, hipSt
     return run_gemv_shape<TV, 8, 1, true, true>(p, g.wpb, stream);
 }
 
+// One token on rows of 65..512 aligned chunks: w4a16_gemv_ks, four rows per
+// workgroup while that leaves two workgroups per CU, else two or one
+template <int TV>
+bool try_gemv_ks(const GemvParams& p, bool aligned, int cus, hipStream_t stream, clove_status_t* st) {
+    const int ks = cdiv(p.nch, 64);
+    if (TV != 1 || !aligned || !aligned16(p.X) || ks < 2 || ks > 8) return false;
+    const int rpw = cdiv(p.O, 4) >= 2 * cus ? 4 : cdiv(p.O, 2) >= cus ? 2 : 1;
+    const dim3 grid(cdiv(p.O, rpw)), block(64 * ks);
+    if (rpw == 4) CLOVE_LAUNCH(w4a16_gemv_ks<4>, grid, block, 0, stream, p);
+    else if (rpw == 2) CLOVE_LAUNCH(w4a16_gemv_ks<2>, grid, block, 0, stream, p);
+    else CLOVE_LAUNCH(w4a16_gemv_ks<1>, grid, block, 0, stream, p);
+    *st = check_launch();
+    return true;
+}
+
 template <int TV>
 clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    clove_status_t kst;
+    if (try_gemv_ks<TV>(p, aligned, cus, stream, &kst)) return kst;
     GemvShape g = gemv_shape(p.O, p.nch, cus);
     // one token on rows of two or more chunks per lane: workgroups halved until
     // there are four per CU (rows of two chunks) or two (longer rows); cold:
