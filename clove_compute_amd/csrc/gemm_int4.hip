@@ -375,6 +375,90 @@ __global__ void __launch_bounds__((gemv_max_threads<NV, ALIGNED, 4>())) int4_gem
     }
 }
 
+// One column, group-wise, on rows of 65..128 aligned chunks (K % 32 == 0,
+// K = 2080..4096): the KS = ceil(nch / 64) = 2 waves of a workgroup share RPW
+// rows of A and split K, wave w taking chunk 64 w + lane of every row.  The lane turns its own 32
+// bytes of B (one byte per k, the column in the high nibble) into the four
+// nibble words in A's order, their sum and the group's zB / sB in registers --
+// nothing is staged in LDS, and that work serves RPW rows -- then forms
+// each row's exact chunk partial P as in int4_gemv and (sA sB) * P; each wave
+// sums its lanes (the fixed butterfly) and wave 0 adds the KS partials of a
+// row in wave order.  Cold graph replays, us per call, against int4_gemv:
+// 11008 x 4096 6.83 -> 6.16, 14336 x 4096 8.34 -> 7.15, 11008 x 2304 6.06 ->
+// 5.40, 4096 x 4096 4.22 -> 4.18; four rows per workgroup ahead of one, two
+// and eight (11008 x 4096: 7.54 / 6.34 / 6.37).  Longer rows (KS 3..8) stay on
+// int4_gemv, which measured as fast or faster there (4096 x 11008 6.40 against
+// 6.39, 4096 x 14336 7.06 against 7.21, 8192 x 8192 7.80 against 7.71 at best).
+// (KS is read from the block size; part[] has room for 8)
+template <int RPW>
+__global__ void __launch_bounds__(512) int4_gemv_ks(GemvParams p) {
+    __shared__ float part[8][RPW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int KS = blockDim.x >> 6;
+    const int nch = p.nch, K = p.K, G = p.G;
+    const int row0 = blockIdx.x * RPW;
+    const int c = wave * 64 + lane;
+    const int cs = min(c, nch - 1);  // lanes past the end: garbage, masked by sA = 0
+    const u32x4 b0 = *reinterpret_cast<const u32x4*>(p.B + 32 * cs);
+    const u32x4 b1 = *reinterpret_cast<const u32x4*>(p.B + 32 * cs + 16);
+    const uint16_t bz = p.B_zero[cs >> 2], bs = p.B_scale[cs >> 2];
+    u32x4 a[RPW];
+    uint16_t sah[RPW], zah[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = min(row0 + r, p.M - 1);
+        a[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.A + (int64_t)row * (K / 2) + 16 * cs));
+        const int64_t gi = (int64_t)row * G + (cs >> 2);
+        sah[r] = p.A_scale[gi];
+        zah[r] = p.A_zero[gi];
+    }
+    // B nibble words in A's order: byte j of word d holds k = 8d + 2j (high) and 8d + 2j + 1 (low)
+    const unsigned v[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    unsigned bw[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const unsigned ev = __builtin_amdgcn_perm(v[2 * d + 1], v[2 * d], 0x06040200u);
+        const unsigned od = __builtin_amdgcn_perm(v[2 * d + 1], v[2 * d], 0x07050301u);
+        bw[d] = (ev & 0xf0f0f0f0u) | ((od >> 4) & 0x0f0f0f0fu);
+    }
+    unsigned sb = __builtin_amdgcn_udot8(bw[0], kOnes, 0u, false);
+    sb = __builtin_amdgcn_udot8(bw[1], kOnes, sb, false);
+    sb = __builtin_amdgcn_udot8(bw[2], kOnes, sb, false);
+    sb = __builtin_amdgcn_udot8(bw[3], kOnes, sb, false);
+    const int zb = (int)rintf(h2f(bz));
+    const int sbz = (int)sb - 32 * zb;  // sum (qB - zB) over the chunk
+    const float sbf = h2f(bs);
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const bool valid = row0 + r < p.M && c < nch;
+        const u32x4 av = a[r];
+        unsigned sa = __builtin_amdgcn_udot8(av.x, kOnes, 0u, false);
+        sa = __builtin_amdgcn_udot8(av.y, kOnes, sa, false);
+        sa = __builtin_amdgcn_udot8(av.z, kOnes, sa, false);
+        sa = __builtin_amdgcn_udot8(av.w, kOnes, sa, false);
+        unsigned dot = __builtin_amdgcn_udot8(av.x, bw[0], 0u, false);
+        dot = __builtin_amdgcn_udot8(av.y, bw[1], dot, false);
+        dot = __builtin_amdgcn_udot8(av.z, bw[2], dot, false);
+        dot = __builtin_amdgcn_udot8(av.w, bw[3], dot, false);
+        const int za = (int)rintf(h2f(zah[r]));
+        const float fa = valid ? h2f(sah[r]) : 0.0f;
+        // |terms| < 2^24 for zero points in [-255, 255]: 24-bit products are exact
+        const int P = (int)dot - __mul24(zb, (int)sa) - __mul24(za, sbz);
+        acc[r] = wave_sum((fa * sbf) * (float)P);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) part[wave][r] = acc[r];
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= RPW) return;
+    float t = part[0][lane];
+    for (int w = 1; w < KS; ++w) t += part[w][lane];
+    const int row = row0 + lane;
+    if (row < p.M) p.C[row] = f2h(t);
+}
+
 // ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
@@ -449,8 +533,27 @@ clove_status_t run_gemv(const GemvParams& p, bool aligned, int cus, hipStream_t 
     return run_gemv_shape<NV, MODE, 8, 1, true>(p, g.wpb, stream);
 }
 
+// One group-wise column on rows of 65..128 aligned chunks: int4_gemv_ks, four
+// rows per workgroup while that leaves two workgroups per CU, else two or one
+bool try_gemv_ks(const GemvParams& p, bool aligned, int cus, hipStream_t stream, clove_status_t* st) {
+    const int ks = cdiv(p.nch, 64);
+    if (p.N != 1 || !aligned || p.ldb != 1 || (reinterpret_cast<uintptr_t>(p.B) & 15) != 0 || ks != 2)
+        return false;
+    const int rpw = cdiv(p.M, 4) >= 2 * cus ? 4 : cdiv(p.M, 2) >= cus ? 2 : 1;
+    const dim3 grid(cdiv(p.M, rpw)), block(64 * ks);
+    if (rpw == 4) CLOVE_LAUNCH(int4_gemv_ks<4>, grid, block, 0, stream, p);
+    else if (rpw == 2) CLOVE_LAUNCH(int4_gemv_ks<2>, grid, block, 0, stream, p);
+    else CLOVE_LAUNCH(int4_gemv_ks<1>, grid, block, 0, stream, p);
+    *st = check_launch();
+    return true;
+}
+
 template <int MODE>
 clove_status_t gemv_by_n(const GemvParams& p, bool aligned, int cus, hipStream_t stream) {
+    if constexpr (MODE == mg::kI4Groupwise) {
+        clove_status_t kst;
+        if (try_gemv_ks(p, aligned, cus, stream, &kst)) return kst;
+    }
     if (p.N == 1) return run_gemv<1, MODE>(p, aligned, cus, stream);
     if (p.N == 2) return run_gemv<2, MODE>(p, aligned, cus, stream);
     if (p.N <= 4) return run_gemv<4, MODE>(p, aligned, cus, stream);
