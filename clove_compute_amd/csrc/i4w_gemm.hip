@@ -29,6 +29,14 @@ using CfgC32 = Cfg<2, 1, 1, 1, 4>;  // 64 x 32, 2 waves (several workgroups per 
 // T = 2048: 184.2 -> 166.2 and 470.8 -> 420.1; at T <= 256 it loses (T = 64:
 // 14.6 -> 19.3)
 using CfgS64 = Cfg<4, 1, 2, 2, 2>;
+// 256 x 128 with eight waves of 64 x 64 (two per SIMD), one stage ahead
+// (100 KB LDS, one workgroup per CU): the fused gate/up + SwiGLU once these
+// tiles alone cover 3/4 of the CUs (never split: the kernel has no split-K
+// path for eight waves).  Llama-1B MLP T = 512 (I x K = 8192 x 2048, graph-free
+// timing of 30 calls, cold weights): 48.6 us with 256 x 64 -> 40.6 us; with
+// two stages ahead 42.4.  The one-projection shapes measured slower on it
+// (they need split K at T = 512)
+using CfgS128 = Cfg<4, 2, 2, 2, 2>;
 
 inline size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
@@ -45,7 +53,7 @@ Plan make_plan(int R, int C, int G, int cus, int target, int min_groups) {
     pl.tiles_r = cdiv(R, CF::BR);
     pl.tiles_c = cdiv(C, CF::BC);
     const int tiles = pl.tiles_r * pl.tiles_c;
-    int ns = 4 * tiles >= 3 * cus ? 1 : target / tiles;
+    int ns = 4 * tiles >= 3 * cus || CF::NW == 8 ? 1 : target / tiles;
     ns = max(1, min(ns, G / min_groups));
     pl.gps = cdiv(G, ns);
     pl.nsplit = cdiv(G, pl.gps);
@@ -91,13 +99,18 @@ clove_status_t run(Args a, int cus, int target, int min_groups, size_t extra_byt
 //   otherwise 128 x 64 with two workgroups per CU, whose waves interleave
 //   VALU (unpack, fold) with MFMA -- ahead of 128 x 128 by 15-25 % on the
 //   INT4 N = 128 and W4A16 T = 512 shapes -- unless 256 x 128 tiles already
-//   cover the CUs (large prefill); the fused SwiGLU from 512 X rows up: 256 x 64
+//   cover the CUs (large prefill); the fused SwiGLU from 512 X rows up: 256 x
+//   128 with eight waves where those tiles cover 3/4 of the CUs, else 256 x 64
 // Splits keep at least 10 (64 x 32) or 8 groups each.
 template <bool XS, int OUT, class Prep>
 clove_status_t by_shape(const Args& a, int cus, size_t extra_bytes, hipStream_t stream, Prep prep) {
     const int rows = OUT == 2 ? 2 * a.R : a.R;  // weight rows
     if (a.C <= 32) return run<CfgC32, XS, OUT>(a, cus, 3 * cus, 10, extra_bytes, stream, prep);
-    if (OUT == 2 && a.C >= 512) return run<CfgS64, XS, OUT>(a, cus, 2 * cus, 8, extra_bytes, stream, prep);
+    if (OUT == 2 && a.C >= 512) {
+        if (4 * cdiv(rows, CfgS128::BR) * cdiv(a.C, CfgS128::BC) >= 3 * cus)
+            return run<CfgS128, XS, OUT>(a, cus, cus, 8, extra_bytes, stream, prep);
+        return run<CfgS64, XS, OUT>(a, cus, 2 * cus, 8, extra_bytes, stream, prep);
+    }
     // (SwiGLU tiles pair gate and up rows: the same outputs take twice the
     // weight rows, so the big tile waits for twice the grid)
     if (cdiv(rows, CfgBig::BR) * cdiv(a.C, CfgBig::BC) >= (OUT == 2 ? 2 : 1) * cus)

@@ -92,7 +92,7 @@ struct Cfg {
     static constexpr int DW = W_BYTES / (1024 * NW);    // weight DMA instructions
     static constexpr int DS = 2 * BR / (64 * NW);       // scale + zero DMA instructions
     static_assert(KS == 8 || KS == 4, "k-steps per stage");
-    static_assert(NW == 2 || NW == 4, "waves");
+    static_assert(NW == 2 || NW == 4 || NW == 8, "waves");
     static_assert(X_BYTES % (1024 * NW) == 0 && W_BYTES % (1024 * NW) == 0 && (2 * BR) % (64 * NW) == 0,
                   "DMA split");
     static_assert(BC <= 64 * NW, "one dword of sx per lane covers the tile");
@@ -383,7 +383,9 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     }
 
     }  // stages of one group
-    // ---- split-K: publish, the last arriver sums all partials in split order ----
+    // ---- split-K: publish, the last arriver sums all partials in split order
+    // (not with eight waves: their host plan never splits K) ----
+    if constexpr (CF::NW <= 4) {
     if (p.nsplit > 1) {
         constexpr int NC = FW * FX * 4;  // f32x4 chunks per thread
         f32x4 v[NC];
@@ -409,6 +411,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
                 for (int q = 0; q < 4; ++q)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = v[(i * FX + j) * 4 + q][e];
+    }
     }
 
     // ---- epilogue ----

@@ -127,12 +127,14 @@ def check_rows(X, Wq, s, z, H, rows):
 
 
 # T <= 4: GEMV; T > 4 with K % 128 == 0: the MFMA GEMM (64x32 tiles up to 32
-# tokens, 128x64 / 256x128 above, with and without split K); the Llama-1B
-# MLP (I = 8192, K = 2048) at decode and prefill
+# tokens, 128x64 / 256x128 above, with and without split K; from 512 tokens
+# 256x64, or 256x128 with eight waves where those tiles cover 3/4 of the CUs:
+# the Llama-1B MLP at T = 512 and the ragged 1000 x 3000); the Llama-1B MLP
+# (I = 8192, K = 2048) at decode and prefill
 @pytest.mark.parametrize("T,I,K", [(1, 8192, 2048), (2, 300, 1024), (3, 64, 256), (4, 1000, 4096),
                                    (5, 8192, 2048), (17, 200, 512), (33, 1000, 1024), (64, 96, 2048),
                                    (100, 777, 384), (512, 8192, 2048), (1, 2000, 4096), (1, 1100, 8192),
-                                   (600, 520, 1024), (1030, 136, 256)])
+                                   (600, 520, 1024), (1030, 136, 256), (1000, 3000, 256)])
 def test_w4a16_swiglu_shapes(T, I, K):
     X, Wq, s, z, g = make_gate_up(T, I, K, "shapes")
     H = run_w4a16_swiglu(X, Wq, s, z, I)
@@ -150,7 +152,7 @@ def test_w4a16_swiglu_composed_fallback(T, I, K, x_offset):
 
 
 @pytest.mark.parametrize("T,I,K", [(1, 512, 1024), (4, 96, 256), (48, 256, 512), (300, 640, 768),
-                                   (512, 640, 768)])
+                                   (512, 640, 768), (1024, 3072, 256)])
 def test_w4a16_swiglu_exact_inputs(T, I, K):
     # gate and up are exact: the only freedom left is expf's last fp32 bit
     X, Wq, s, z, _ = make_gate_up(T, I, K, "pow2", pow2=True)
