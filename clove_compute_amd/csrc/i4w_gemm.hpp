@@ -35,8 +35,8 @@
 // Staging.  Everything a stage needs arrives by LDS DMA (inline asm, so that
 // the compiler does not wait for all DMAs before each LDS read; completion is
 // tracked with explicit vmcnt waits and one barrier per stage):
-//   X   BC rows x 256 B, 16-byte chunk c of row x at slot c ^ (x & 7)
-//   W   BR rows x 64 B,  chunk c of row r at slot c ^ ((r >> 1) & 3)
+//   X   BC rows x 256 B, 16-byte chunk c of row x at slot c ^ (x & 15)
+//   W   BR rows x 64 B,  chunk c of row r at slot c ^ ((r >> 2) & 3)
 //   SC  BR dwords, the aligned dword holding sw[r, g]   (half chosen by parity)
 //   ZR  BR dwords, the same for zw[r, g]
 //   XS  64 NW fp32 of sx[g, c0 ...]                     (INT4 only)
@@ -148,11 +148,22 @@ __device__ __forceinline__ f16x8 unpack8(unsigned w, f16x2 zz) {
     return r;
 }
 
-// weight rows of 64 bytes (whole group) or 32 bytes (half): the 8 lanes of a
-// fragment read (8 consecutive rows, one chunk each) hit 8 bank groups
+// A 16-byte LDS read serves 16 lanes per clock from one 256-byte window of
+// banks.  The 16 lanes of a fragment read take 16 consecutive rows, one chunk
+// each, so the chunk is swizzled by the row bits above those that already
+// separate rows within a window:
+//   weight rows of 64 bytes (whole group: 4 rows per window) or 32 bytes
+//   (half: 8 per window): chunk c at c ^ ((r >> 2) & 3) or c ^ ((r >> 3) & 1)
+//   X rows of 256 bytes (one per window) or 128 bytes (two): chunk c at
+//   c ^ (x & 15) or c ^ ((x >> 1) & 7)
+// so rows r .. r + 15 reading one chunk hit 16 distinct 16-byte bank slots.
 template <int KS>
 __device__ __forceinline__ int swz_w(int r) {
-    return KS == 8 ? ((r >> 1) & 3) : ((r >> 2) & 1);
+    return KS == 8 ? ((r >> 2) & 3) : ((r >> 3) & 1);
+}
+template <int KS>
+__device__ __forceinline__ int swz_x(int x) {
+    return KS == 8 ? (x & 15) : ((x >> 1) & 7);
 }
 
 template <int IMM>
@@ -213,7 +224,7 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     for (int i = 0; i < CF::DX; ++i) {
         constexpr int CPR = CF::XRB / 16;  // chunks per X row
         const int row = (1024 / CF::XRB) * (wave * CF::DX + i) + lane / CPR;
-        offx[i] = (c0 + row) * K * 2 + 16 * ((lane % CPR) ^ (row & 7));
+        offx[i] = (c0 + row) * K * 2 + 16 * ((lane % CPR) ^ swz_x<KS>(row));
     }
 #pragma unroll
     for (int i = 0; i < CF::DW; ++i) {
@@ -257,14 +268,13 @@ __global__ void __launch_bounds__(CF::NT) i4w_gemm(Args p) {
     // ---- fragment addressing.  Rows of a lane differ between tiles by a
     // multiple of 32, which leaves the swizzle (low row bits) unchanged, so
     // per k-step one per-lane offset serves every tile and the tile enters as
-    // an immediate: X row x, step s at 256 x + 16 ((8 h + s) ^ (x & 7)), with
-    // (8 h + s) ^ (x & 7) = 8 h + (s ^ (lane & 7)); weight row r, half e at
-    // 64 r + 16 ((2 h + e) ^ ((lane >> 1) & 3)).
+    // an immediate: X row x, step s at 256 x + 16 ((8 h + s) ^ (x & 15));
+    // weight row r, half e at 64 r + 16 ((2 h + e) ^ ((r >> 2) & 3)).
     const int h = lane >> 5, l32 = lane & 31;
     const int xrow0 = wc * 32 * FX + l32, wrow0 = wr * 32 * FW + l32;
     unsigned xoff[8];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) xoff[s] = xrow0 * CF::XRB + 16 * ((KS * h + s) ^ (lane & 7));
+    for (int s = 0; s < KS; ++s) xoff[s] = xrow0 * CF::XRB + 16 * ((KS * h + s) ^ swz_x<KS>(xrow0));
     constexpr int NWC = KS / 4;  // 16-byte weight chunks per lane per stage
     unsigned woff[NWC];
 #pragma unroll
