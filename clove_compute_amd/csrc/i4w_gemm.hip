@@ -275,6 +275,27 @@ bool try_i4w_int4(const Int4Args& q, int cus, hipStream_t stream, clove_status_t
     return true;
 }
 
+// Weight rows per workgroup of the raw-B stream, 16 WF (WF = 1..3): the fewest
+// rows on the busiest CU, counting whole rounds of workgroups; on a tie the
+// larger workgroups when each has four or more K-slice waves (G > 16), else
+// the smaller.  Cold graph replays, us per call for WF = 1 / 2 / 3 (N = 16):
+// 11008 x 4096 9.57 / 11.23 / 9.09, 11008 x 8192 19.73 / 20.62 / 15.90,
+// 8192 x 4096 7.58 / 7.30 / 8.66, 16384 x 4096 12.06 / 11.17 / 14.40,
+// 4096 x 4096 5.52 / 6.87 / 8.29, 14336 x 2048 7.48 / 9.15 / 11.13, 11008 x
+// 2048 7.17 / 8.98 / 7.81: the rule picks the fastest of the three in each.
+int rawb_wf(int R, int G, int cus) {
+    int best = 1;
+    int64_t best_rows = -1;
+    for (int wf = 1; wf <= 3; ++wf) {
+        const int64_t rows = (int64_t)cdiv(cdiv(R, 16 * wf), cus) * wf;
+        if (best_rows < 0 || rows < best_rows || (rows == best_rows && G > 16)) {
+            best = wf;
+            best_rows = rows;
+        }
+    }
+    return best;
+}
+
 bool try_i4w_int4_rawb(const Int4Args& q, int cus, hipStream_t stream, clove_status_t* status) {
     // 15 or 16 columns: B rows are 8 bytes, read in place (no transpose pass)
     const int G = q.K / 128;
@@ -296,8 +317,10 @@ bool try_i4w_int4_rawb(const Int4Args& q, int cus, hipStream_t stream, clove_sta
     a.N = q.N;
     a.alpha = 1.0f;
     a.beta = 0.0f;
-    *status = cdiv(a.R, 32) >= cus ? stream_by_k<2, 1, true, 0, true>(a, stream)
-                                   : stream_by_k<1, 1, true, 0, true>(a, stream);
+    const int wf = rawb_wf(a.R, G, cus);
+    *status = wf == 3   ? stream_by_k<3, 1, true, 0, true>(a, stream)
+              : wf == 2 ? stream_by_k<2, 1, true, 0, true>(a, stream)
+                        : stream_by_k<1, 1, true, 0, true>(a, stream);
     return true;
 }
 

@@ -71,10 +71,12 @@ def test_config4_groupwise(M, N, K):
 
 # (N = 1 with K = 2080..4096 takes the GEMV whose two waves split K, with one,
 # two or four rows per workgroup: 300, 1030 and 2050 rows, the last workgroup
-# ragged; K = 2304 leaves lanes of the second wave without a chunk)
+# ragged; K = 2304 leaves lanes of the second wave without a chunk.  N = 16
+# takes the raw-B streaming kernel with 48 rows per workgroup at 11000 rows
+# and 32 at 8000, both ragged)
 @pytest.mark.parametrize("M,N,K", [(300, 1, 4096), (260, 8, 2048), (100, 16, 1024), (130, 128, 512),
                                    (64, 3, 640), (1024, 4, 11008), (512, 8, 4096), (96, 6, 4104),
-                                   (2050, 1, 4096), (1030, 1, 2304)])
+                                   (2050, 1, 4096), (1030, 1, 2304), (11000, 16, 4096), (8000, 16, 4096)])
 def test_groupwise_pow2_bit_exact(M, N, K):
     # power-of-two scales, values q-z in [-1, 1]: every fp32/fp16 step is exact
     A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2", pow2=True, small=True)
