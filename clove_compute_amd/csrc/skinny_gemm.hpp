@@ -26,6 +26,12 @@
 // the CUs, with the shared publish / reduce (split order, deterministic;
 // int32 partials for INT8, so the integer accumulator stays exact).
 //
+// K slices (KW > 1, FP16 only, no split K): the small products (short K, a
+// 32x32 tile per CU or fewer) run 32x32 tiles whose four waves each take one
+// of every K tile's four k-steps; after the K loop every wave stores its sums
+// to LDS and each wave adds the four slices, in slice order, for a quarter of
+// the tile's output runs.
+//
 // Two B operands (NB = 2, FP16 only): B and B2 share A and the tile's
 // columns; each stage holds A, then the B tile, then the B2 tile, and every
 // wave keeps both accumulator sets.  The SwiGLU epilogue (kF16SwiGLU) then
