@@ -76,9 +76,13 @@ def test_config4_groupwise(M, N, K):
 # and 32 at 8000, both ragged)
 @pytest.mark.parametrize("M,N,K", [(300, 1, 4096), (260, 8, 2048), (100, 16, 1024), (130, 128, 512),
                                    (64, 3, 640), (1024, 4, 11008), (512, 8, 4096), (96, 6, 4104),
-                                   (2050, 1, 4096), (1030, 1, 2304), (11000, 16, 4096), (8000, 16, 4096)])
+                                   (2050, 1, 4096), (1030, 1, 2304), (11000, 16, 4096), (8000, 16, 4096),
+                                   (130, 1, 2080), (70, 1, 4128)])
 def test_groupwise_pow2_bit_exact(M, N, K):
     # power-of-two scales, values q-z in [-1, 1]: every fp32/fp16 step is exact
+    # (N = 1 on rows of 65..128 chunks of 32 k takes the two-wave K-split GEMV:
+    # K = 2080 is its lower bound, the second wave holding one chunk, and K =
+    # 4128 is just past its upper one)
     A_q, sA, zA, B_q, sB, zB = make_case(M, N, K, "pow2", pow2=True, small=True)
     C = run_int4(A_q, sA, zA, B_q, sB, zB, M, N, K)
     Cr, ref, _ = oracle.gemm_int4_groupwise(A_q, sA, zA, B_q, sB, zB, M, N, K)

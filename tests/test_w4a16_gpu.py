@@ -64,13 +64,15 @@ def test_llama1b_layer(T, name, O, K, beta):
                                    (4, 2048, 4096), (3, 520, 1024),
                                    (4, 256, 8192), (64, 512, 1024),
                                    (300, 136, 256), (4, 300, 11008), (2, 520, 16384),
-                                   (1, 6000, 2048), (1, 1031, 4096), (1, 2051, 8192), (1, 1000, 16384)])
+                                   (1, 6000, 2048), (1, 1031, 4096), (1, 2051, 8192), (1, 1000, 16384),
+                                   (1, 130, 2080), (1, 70, 16416)])
 def test_pow2_bit_exact(T, O, K):
     # (T = 2..4 on long rows: more X pieces than the GEMV's prefetch holds;
     # one token: X per lane in registers with one to four rows per wave (6000
     # rows: two), and the waves of a workgroup splitting K with one, two or
     # four rows per workgroup, the last one ragged (1031, 2051), up to eight
-    # waves (K = 16384))
+    # waves (K = 16384); the bounds of that form: 65 chunks, the second wave
+    # holding one (K = 2080), and 513 chunks, past it (K = 16416))
     X, W, s, z, _ = make(T, O, K, "pow2", pow2=True)
     Y = run(X, W, s, z, None, O)
     _, ref = oracle.w4a16(X, W, s, z)
