@@ -289,7 +289,7 @@ def test_k_sliced_small_tiles(M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(7, 4096, 4096), (100, 264, 640), (128, 4096, 4096),
                                    (3, 4096, 4096), (2, 11008, 4096), (4, 4096, 11008),
-                                   (512, 512, 1024), (3, 8192, 1024)])
+                                   (512, 512, 1024), (3, 8192, 1024), (128, 4096, 11008)])
 def test_skinny_small_integers_bit_exact(M, N, K):
     # |a|, |b| <= 4 integers: every product and partial sum is exact in fp32,
     # so split K and the fp16 output are exact (M = 2..4 on these weights
